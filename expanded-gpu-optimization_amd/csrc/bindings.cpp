@@ -1,0 +1,111 @@
+// fused_hoad._C: the torch-facing boundary of the MI355X kernels.
+//
+// Same module name, functions, argument names, defaults, return order, check order and
+// messages as /root/reference/csrc/bindings.cpp:9-66, so Python callers and their tests see
+// the same API. Each call validates the tensors, allocates outputs (and the backward's
+// workspace) with the torch caching allocator on the inputs' device, and enqueues the kernels
+// on the current stream through the C ABI in include/fused_hoad.h. No host synchronization.
+#include <torch/extension.h>
+
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+#include <c10/core/DeviceGuard.h>
+
+#include <vector>
+
+#include "fused_hoad.h"
+
+namespace {
+
+constexpr int64_t kParameterCount = 12737;
+
+// Check order and messages follow /root/reference/csrc/bindings.cpp:9-24. PyTorch-ROCm
+// tensors report device type "cuda", hence the CUDA wording.
+void check_inputs(const torch::Tensor& coordinates, const torch::Tensor& parameters) {
+  TORCH_CHECK(coordinates.is_cuda(), "coordinates must be a CUDA tensor");
+  TORCH_CHECK(parameters.is_cuda(), "parameters must be a CUDA tensor");
+  TORCH_CHECK(coordinates.is_contiguous(), "coordinates must be contiguous");
+  TORCH_CHECK(parameters.is_contiguous(), "parameters must be contiguous");
+  TORCH_CHECK(coordinates.scalar_type() == torch::kFloat32, "coordinates must use float32");
+  TORCH_CHECK(parameters.scalar_type() == torch::kFloat32, "parameters must use float32");
+  TORCH_CHECK(coordinates.dim() == 2 && coordinates.size(1) == 2,
+              "coordinates must have shape [batch, 2]");
+  TORCH_CHECK(parameters.dim() == 1 && parameters.numel() == kParameterCount,
+              "parameters must have shape [12737]");
+  TORCH_CHECK(coordinates.device() == parameters.device(),
+              "coordinates and parameters must be on the same device");
+}
+
+void check_status(int status) {
+  TORCH_CHECK(status == FHOAD_SUCCESS, "fused_hoad kernel error (", fhoad_status_string(status),
+              "): ", fhoad_last_error());
+}
+
+void* current_stream(const torch::Tensor& tensor) {
+  return static_cast<void*>(
+      at::hip::getCurrentHIPStreamMasqueradingAsCUDA(tensor.get_device()).stream());
+}
+
+}  // namespace
+
+std::vector<torch::Tensor> fused_forward_laplacian(torch::Tensor coordinates,
+                                                   torch::Tensor parameters, int64_t version) {
+  TORCH_CHECK(version >= 0 && version <= 5, "version must be 0 to 5");
+  check_inputs(coordinates, parameters);
+  const c10::DeviceGuard device_guard(coordinates.device());
+  const int64_t batch = coordinates.size(0);
+  auto output = torch::empty({batch, 1}, coordinates.options());
+  auto laplacian = torch::empty({batch, 1}, coordinates.options());
+  if (batch == 0) {
+    return {output, laplacian};
+  }
+  check_status(fhoad_forward_laplacian(coordinates.data_ptr<float>(), parameters.data_ptr<float>(),
+                                       output.data_ptr<float>(), laplacian.data_ptr<float>(),
+                                       batch, static_cast<int>(version),
+                                       current_stream(coordinates)));
+  return {output, laplacian};
+}
+
+std::vector<torch::Tensor> fused_forward_laplacian_backward(torch::Tensor coordinates,
+                                                            torch::Tensor parameters,
+                                                            torch::Tensor grad_output,
+                                                            torch::Tensor grad_laplacian,
+                                                            int64_t version) {
+  TORCH_CHECK(version >= 1 && version <= 6, "backward version must be 1 to 6");
+  check_inputs(coordinates, parameters);
+  for (const auto& grad : {grad_output, grad_laplacian}) {
+    TORCH_CHECK(grad.is_cuda() && grad.is_contiguous() && grad.scalar_type() == torch::kFloat32,
+                "upstream gradients must be contiguous float32 CUDA tensors");
+    TORCH_CHECK(grad.numel() == coordinates.size(0), "upstream gradients must have [batch] values");
+    TORCH_CHECK(grad.device() == coordinates.device(),
+                "upstream gradients must be on the coordinates' device");
+  }
+  const c10::DeviceGuard device_guard(coordinates.device());
+  const int64_t batch = coordinates.size(0);
+  auto grad_coordinates = torch::empty_like(coordinates);
+  if (batch == 0) {
+    return {torch::zeros_like(parameters), grad_coordinates};
+  }
+  auto grad_parameters = torch::empty_like(parameters);
+  const size_t workspace_bytes = fhoad_backward_workspace_size(batch);
+  auto workspace = torch::empty({static_cast<int64_t>(workspace_bytes)},
+                                coordinates.options().dtype(torch::kUInt8));
+  check_status(fhoad_forward_laplacian_backward(
+      coordinates.data_ptr<float>(), parameters.data_ptr<float>(), grad_output.data_ptr<float>(),
+      grad_laplacian.data_ptr<float>(), grad_parameters.data_ptr<float>(),
+      grad_coordinates.data_ptr<float>(), workspace.data_ptr(), workspace_bytes, batch,
+      static_cast<int>(version), current_stream(coordinates)));
+  return {grad_parameters, grad_coordinates};
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
+  module.def("fused_forward_laplacian", &fused_forward_laplacian,
+             "Fixed MLP forward pass and input Laplacian (MI355X HIP kernel)",
+             pybind11::arg("coordinates"), pybind11::arg("parameters"),
+             pybind11::arg("version") = 2);
+  module.def("fused_forward_laplacian_backward", &fused_forward_laplacian_backward,
+             "Gradients of the fused forward Laplacian w.r.t. parameters and coordinates "
+             "(MI355X HIP kernels)",
+             pybind11::arg("coordinates"), pybind11::arg("parameters"),
+             pybind11::arg("grad_output"), pybind11::arg("grad_laplacian"),
+             pybind11::arg("version") = 6);
+}

@@ -1,0 +1,129 @@
+"""Fused backend: the whole forward Laplacian in one gfx950 kernel launch.
+
+Fixed to the Poisson contract (2 -> 64x4 -> 1 tanh, FP32, on the GPU). The forward is one
+kernel; the backward is the fused HIP kernel pair (default) or, when asked for by name, the
+reference's PyTorch recompute-and-differentiate path. Behaviour follows
+/root/reference/src/fused_hoad/backends/fused.py:24-138.
+"""
+
+from __future__ import annotations
+
+import weakref
+
+import torch
+from torch import Tensor, nn
+
+from fused_hoad._extension import fused_forward_laplacian, fused_forward_laplacian_backward
+from fused_hoad.backends.forward_laplacian import tanh_mlp_forward_laplacian
+from fused_hoad.parameters import (
+    POISSON_PARAMETER_LAYOUT,
+    pack_poisson_parameters,
+    unpack_poisson_parameters,
+)
+
+# Backward modes. Every "cuda*" name runs the same fused HIP backward (the reference's kernel
+# versions are kept as names only); "recompute" is the PyTorch reference backward.
+_CUDA_BACKWARD_VERSIONS = {
+    "cuda": 6,
+    "cuda_v1": 1,
+    "cuda_v2": 2,
+    "cuda_v3": 3,
+    "cuda_v4": 4,
+    "cuda_v5": 5,
+}
+BACKWARD_MODES = (*_CUDA_BACKWARD_VERSIONS, "recompute")
+
+_cache: dict[str, object] = {}
+
+
+class FusedForwardLaplacian(torch.autograd.Function):
+    """Fused-kernel forward; fused-kernel (or, by name, recompute) backward."""
+
+    @staticmethod
+    def forward(ctx, coordinates: Tensor, parameters: Tensor, version: int, backward: str):
+        ctx.save_for_backward(coordinates, parameters)
+        ctx.backward_mode = backward
+        return fused_forward_laplacian(coordinates, parameters, version)
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor, grad_laplacian: Tensor):
+        coordinates, parameters = ctx.saved_tensors
+        needs_coordinates, needs_parameters = ctx.needs_input_grad[:2]
+        mode = ctx.backward_mode
+        if mode in _CUDA_BACKWARD_VERSIONS:
+            grad_parameters, grad_coordinates = fused_forward_laplacian_backward(
+                coordinates, parameters, grad_output, grad_laplacian, _CUDA_BACKWARD_VERSIONS[mode]
+            )
+            return (
+                grad_coordinates if needs_coordinates else None,
+                grad_parameters if needs_parameters else None,
+                None,
+                None,
+            )
+        grad_coordinates, grad_parameters = _recompute_backward(
+            coordinates, parameters, grad_output, grad_laplacian, needs_coordinates, needs_parameters
+        )
+        return grad_coordinates, grad_parameters, None, None
+
+
+def _recompute_backward(
+    coordinates: Tensor,
+    parameters: Tensor,
+    grad_output: Tensor,
+    grad_laplacian: Tensor,
+    needs_coordinates: bool,
+    needs_parameters: bool,
+) -> tuple[Tensor | None, Tensor | None]:
+    """The reference backward: rebuild the jet in PyTorch from the packed buffer and
+    differentiate it with autograd (/root/reference/src/fused_hoad/backends/fused.py:76-101)."""
+    with torch.enable_grad():
+        x = coordinates.detach().requires_grad_(needs_coordinates)
+        flat = parameters.detach().requires_grad_(needs_parameters)
+        views = unpack_poisson_parameters(flat)
+        linears = [
+            (views[f"{spec.name}.weight"], views[f"{spec.name}.bias"])
+            for spec in POISSON_PARAMETER_LAYOUT
+        ]
+        outputs = tanh_mlp_forward_laplacian(linears, x)
+        wanted = [tensor for tensor, needed in ((x, needs_coordinates), (flat, needs_parameters)) if needed]
+        grads = list(
+            torch.autograd.grad(outputs, wanted, (grad_output, grad_laplacian), allow_unused=True)
+        )
+    grad_coordinates = grads.pop(0) if needs_coordinates else None
+    grad_parameters = grads.pop(0) if needs_parameters else None
+    return grad_coordinates, grad_parameters
+
+
+def _packed_parameters(model: nn.Module) -> Tensor:
+    """Differentiable pack while training; otherwise one cached pack per weight update.
+
+    The parameter list is cached per model behind a weakref (a recycled ``id`` cannot return
+    another model's buffer); a call then only compares the parameters' version counters.
+    """
+    model_ref = _cache.get("model")
+    if model_ref is None or model_ref() is not model:
+        _cache.clear()
+        _cache.update(model=weakref.ref(model), parameters=list(model.parameters()))
+    parameters: list[Tensor] = _cache["parameters"]  # type: ignore[assignment]
+    if torch.is_grad_enabled() and any(p.requires_grad for p in parameters):
+        return pack_poisson_parameters(model, differentiable=True)
+    versions = [p._version for p in parameters]
+    if versions != _cache.get("versions"):
+        _cache.update(versions=versions, packed=pack_poisson_parameters(model))
+    return _cache["packed"]  # type: ignore[return-value]
+
+
+def fused_laplacian(
+    model: nn.Module, coordinates: Tensor, version: int = 2, backward: str = "cuda"
+) -> tuple[Tensor, Tensor]:
+    """``(u, Laplacian u)`` of the fixed Poisson MLP from one gfx950 kernel launch.
+
+    ``backward`` selects the gradient path when autograd is active: any ``"cuda*"`` mode runs
+    the fused HIP backward; ``"recompute"`` runs the PyTorch reference backward.
+    """
+    if backward not in BACKWARD_MODES:
+        raise ValueError(f"backward must be one of {BACKWARD_MODES}")
+    parameters = _packed_parameters(model)
+    if parameters.requires_grad or coordinates.requires_grad:
+        return FusedForwardLaplacian.apply(coordinates.contiguous(), parameters, version, backward)
+    return fused_forward_laplacian(coordinates.contiguous(), parameters, version)

@@ -1,0 +1,102 @@
+"""Packed 12,737-float parameter ABI of the fixed Poisson MLP.
+
+Layout (identical to /root/reference/src/fused_hoad/parameters.py:28-48 and
+/root/reference/csrc/mlp_abi.cuh:8-17): for each linear layer in order, its weight
+``[out, in]`` row-major followed by its bias ``[out]``::
+
+    layer0  W[64, 2]  @0       b[64] @128
+    layer1  W[64, 64] @192     b[64] @4288
+    layer2  W[64, 64] @4352    b[64] @8448
+    layer3  W[64, 64] @8512    b[64] @12608
+    layer4  W[1, 64]  @12672   b[1]  @12736      (12,737 floats)
+
+The kernels read this buffer directly; nothing else about the model crosses the boundary.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor, nn
+
+_SHAPES = ((64, 2), (64, 64), (64, 64), (64, 64), (1, 64))
+
+
+@dataclass(frozen=True, slots=True)
+class ParameterSlice:
+    """Where one linear layer's weight and bias live in the packed buffer."""
+
+    name: str
+    out_features: int
+    in_features: int
+    weight_offset: int
+    bias_offset: int
+
+    @property
+    def weight_elements(self) -> int:
+        return self.out_features * self.in_features
+
+    @property
+    def end_offset(self) -> int:
+        return self.bias_offset + self.out_features
+
+
+def _layout() -> tuple[ParameterSlice, ...]:
+    slices = []
+    cursor = 0
+    for index, (rows, cols) in enumerate(_SHAPES):
+        slices.append(ParameterSlice(f"layer{index}", rows, cols, cursor, cursor + rows * cols))
+        cursor += rows * cols + rows
+    return tuple(slices)
+
+
+POISSON_PARAMETER_LAYOUT: tuple[ParameterSlice, ...] = _layout()
+POISSON_PARAMETER_COUNT: int = POISSON_PARAMETER_LAYOUT[-1].end_offset
+
+
+def _linear_layers(model: nn.Module) -> list[nn.Linear]:
+    return [module for module in model.modules() if isinstance(module, nn.Linear)]
+
+
+def _segments(model: nn.Module) -> list[Tensor]:
+    layers = _linear_layers(model)
+    if len(layers) != len(POISSON_PARAMETER_LAYOUT):
+        raise ValueError(f"expected {len(POISSON_PARAMETER_LAYOUT)} linear layers")
+    segments: list[Tensor] = []
+    for layer, spec in zip(layers, POISSON_PARAMETER_LAYOUT, strict=True):
+        expected = (spec.out_features, spec.in_features)
+        if tuple(layer.weight.shape) != expected:
+            raise ValueError(
+                f"{spec.name}.weight must have shape {expected}, got {tuple(layer.weight.shape)}"
+            )
+        if layer.bias is None or tuple(layer.bias.shape) != (spec.out_features,):
+            raise ValueError(f"{spec.name}.bias must have shape ({spec.out_features},)")
+        segments += [layer.weight.reshape(-1), layer.bias.reshape(-1)]
+    return segments
+
+
+def pack_poisson_parameters(model: nn.Module, *, differentiable: bool = False) -> Tensor:
+    """Pack the fixed 2x64x64x64x64x1 MLP into the kernel ABI layout.
+
+    ``differentiable=True`` returns a ``torch.cat`` of the parameters, so a gradient on the
+    packed buffer flows back to the model; otherwise a detached contiguous copy.
+    (Behaviour of /root/reference/src/fused_hoad/parameters.py:55-84.)
+    """
+    segments = _segments(model)
+    if differentiable:
+        return torch.cat(segments)
+    with torch.no_grad():
+        return torch.cat([segment.detach() for segment in segments]).contiguous()
+
+
+def unpack_poisson_parameters(parameters: Tensor) -> dict[str, Tensor]:
+    """Shaped views ``layerN.weight`` / ``layerN.bias`` into a packed buffer."""
+    if parameters.ndim != 1 or parameters.numel() != POISSON_PARAMETER_COUNT:
+        raise ValueError(f"parameters must have shape [{POISSON_PARAMETER_COUNT}]")
+    views: dict[str, Tensor] = {}
+    for spec in POISSON_PARAMETER_LAYOUT:
+        weight = parameters[spec.weight_offset : spec.bias_offset]
+        views[f"{spec.name}.weight"] = weight.view(spec.out_features, spec.in_features)
+        views[f"{spec.name}.bias"] = parameters[spec.bias_offset : spec.end_offset]
+    return views

@@ -1,0 +1,94 @@
+/*
+ * fused_hoad C ABI: the MI355X (gfx950) forward-Laplacian jet and adjoint-jet backward of
+ * the fixed 2 -> 64 -> 64 -> 64 -> 64 -> 1 FP32 tanh MLP.
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer to contiguous
+ * float32 memory on the device that is current on the calling thread, and `stream` is a
+ * hipStream_t (NULL = that device's default stream). Calls are asynchronous with respect to
+ * the host: they enqueue work on `stream` and return. No call allocates device memory except
+ * where stated; the backward takes its scratch as a caller-owned workspace.
+ *
+ * Parameters use the packed 12,737-float layout of the reference
+ * (/root/reference/csrc/mlp_abi.cuh:8-17, src/fused_hoad/parameters.py:28-48):
+ *   W0[64][2] @0, b0[64] @128, then for hidden layers 1..3: W[64][64] ([out][in]) and b[64]
+ *   at 192 + 4160*(layer-1), then w_out[64] @12672 and b_out @12736.
+ *
+ * Every entry point returns FHOAD_SUCCESS (0) or an fhoad_status code; on failure
+ * fhoad_last_error() returns a message for the calling thread.
+ */
+#ifndef FUSED_HOAD_H_
+#define FUSED_HOAD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FHOAD_ABI_VERSION 1
+#define FHOAD_PARAMETER_COUNT 12737
+
+typedef enum fhoad_status {
+  FHOAD_SUCCESS = 0,
+  FHOAD_ERROR_INVALID_VERSION = 1,   /* version outside the accepted range */
+  FHOAD_ERROR_INVALID_VALUE = 2,     /* null pointer or negative batch */
+  FHOAD_ERROR_MISALIGNED = 3,        /* parameters not 16-byte aligned (backward) */
+  FHOAD_ERROR_WORKSPACE = 4,         /* workspace missing or smaller than required */
+  FHOAD_ERROR_DEVICE = 5             /* the HIP runtime reported an error */
+} fhoad_status;
+
+/* Version of this ABI (FHOAD_ABI_VERSION of the build). */
+int fhoad_abi_version(void);
+
+/* Number of floats in the packed parameter buffer: 12737 (mlp_abi.cuh:16-17). */
+int64_t fhoad_parameter_count(void);
+
+/* Static text for a status code. */
+const char* fhoad_status_string(int status);
+
+/* Message describing the last failed call on the calling thread ("" if none). */
+const char* fhoad_last_error(void);
+
+/*
+ * Forward Laplacian: output[b] = u(x_b) and laplacian[b] = (d2u/dx2 + d2u/dy2)(x_b) for
+ * coordinates [batch][2] (x, y interleaved). output and laplacian each hold `batch` floats.
+ * version 0..5 is accepted for API compatibility and every value runs the same gfx950
+ * kernel. batch == 0 enqueues nothing.
+ *
+ * Replaces fused_forward_laplacian_cuda (/root/reference/csrc/fused_residual.cu:587-643),
+ * which the pybind layer binds at /root/reference/csrc/bindings.cpp:28-36.
+ */
+int fhoad_forward_laplacian(const float* coordinates, const float* parameters, float* output,
+                            float* laplacian, int64_t batch, int version, void* stream);
+
+/*
+ * Bytes of device workspace fhoad_forward_laplacian_backward needs for `batch` points
+ * (per-slot weight-gradient partial rows). 0 for batch <= 0.
+ */
+size_t fhoad_backward_workspace_size(int64_t batch);
+
+/*
+ * Backward of the forward Laplacian. Given dLoss/du (grad_output[batch]) and
+ * dLoss/dLaplacian (grad_laplacian[batch]), writes dLoss/dparameters (grad_parameters[12737],
+ * overwritten, not accumulated) and dLoss/dcoordinates (grad_coordinates[batch][2]).
+ * parameters must be 16-byte aligned. workspace must hold
+ * fhoad_backward_workspace_size(batch) bytes (its contents on entry are ignored). The
+ * weight-gradient sum runs in a fixed order that does not depend on the grid size, so
+ * results are bitwise reproducible. version 1..6 is accepted for API compatibility and every
+ * value runs the same gfx950 kernels. batch == 0 zero-fills grad_parameters.
+ *
+ * Replaces fused_forward_laplacian_backward_cuda (/root/reference/csrc/fused_backward.cu:
+ * 859-934), which the pybind layer binds at /root/reference/csrc/bindings.cpp:38-54.
+ */
+int fhoad_forward_laplacian_backward(const float* coordinates, const float* parameters,
+                                     const float* grad_output, const float* grad_laplacian,
+                                     float* grad_parameters, float* grad_coordinates,
+                                     void* workspace, size_t workspace_bytes, int64_t batch,
+                                     int version, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* FUSED_HOAD_H_ */

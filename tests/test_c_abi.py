@@ -1,0 +1,145 @@
+"""The C ABI (include/fused_hoad.h) of libfused_hoad_hip.so, called directly through ctypes.
+
+CPU part: the library loads, exports every function the header declares, and rejects bad
+arguments before touching a device. GPU part: the raw entry points, driven with device
+pointers and the current stream, give bitwise the same results as fused_hoad._C.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fused_hoad.h"
+LIBRARY = ROOT / "expanded-gpu-optimization_amd" / "fused_hoad" / "libfused_hoad_hip.so"
+
+
+def _lib() -> ctypes.CDLL:
+    assert LIBRARY.exists(), f"{LIBRARY} is not built (run __graft_entry__.build())"
+    lib = ctypes.CDLL(str(LIBRARY))
+    lib.fhoad_abi_version.restype = ctypes.c_int
+    lib.fhoad_parameter_count.restype = ctypes.c_int64
+    lib.fhoad_status_string.restype = ctypes.c_char_p
+    lib.fhoad_status_string.argtypes = [ctypes.c_int]
+    lib.fhoad_last_error.restype = ctypes.c_char_p
+    lib.fhoad_backward_workspace_size.restype = ctypes.c_size_t
+    lib.fhoad_backward_workspace_size.argtypes = [ctypes.c_int64]
+    vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.fhoad_forward_laplacian.restype = ci
+    lib.fhoad_forward_laplacian.argtypes = [vp, vp, vp, vp, i64, ci, vp]
+    lib.fhoad_forward_laplacian_backward.restype = ci
+    lib.fhoad_forward_laplacian_backward.argtypes = [vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, i64, ci, vp]
+    return lib
+
+
+def _declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^[a-z_0-9 ]+\*?\s*(fhoad_[a-z_]+)\(", text, flags=re.MULTILINE)))
+
+
+def test_header_declares_the_entry_points() -> None:
+    assert _declared_functions() == [
+        "fhoad_abi_version",
+        "fhoad_backward_workspace_size",
+        "fhoad_forward_laplacian",
+        "fhoad_forward_laplacian_backward",
+        "fhoad_last_error",
+        "fhoad_parameter_count",
+        "fhoad_status_string",
+    ]
+
+
+def test_library_exports_every_declared_function() -> None:
+    lib = _lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_constants_and_status_strings() -> None:
+    lib = _lib()
+    assert lib.fhoad_abi_version() == 1
+    assert lib.fhoad_parameter_count() == 12737
+    assert lib.fhoad_status_string(0) == b"success"
+    assert lib.fhoad_status_string(4) == b"workspace too small"
+
+
+def test_workspace_size_is_one_partial_row_per_slot() -> None:
+    lib = _lib()
+    assert lib.fhoad_backward_workspace_size(0) == 0
+    row = 12800 * 4
+    assert lib.fhoad_backward_workspace_size(1) == row
+    assert lib.fhoad_backward_workspace_size(64) == row
+    assert lib.fhoad_backward_workspace_size(65) == 2 * row
+    assert lib.fhoad_backward_workspace_size(65536) == 256 * row
+    assert lib.fhoad_backward_workspace_size(1 << 20) == 256 * row
+
+
+def test_argument_errors_are_reported_before_any_device_work() -> None:
+    lib = _lib()
+    assert lib.fhoad_forward_laplacian(None, None, None, None, 4, 7, None) == 1
+    assert b"version must be 0 to 5" in lib.fhoad_last_error()
+    assert lib.fhoad_forward_laplacian(None, None, None, None, -1, 2, None) == 2
+    assert lib.fhoad_forward_laplacian(None, None, None, None, 0, 2, None) == 0
+    assert lib.fhoad_forward_laplacian(None, None, None, None, 4, 2, None) == 2
+    assert lib.fhoad_forward_laplacian_backward(None, None, None, None, None, None, None, 0, 4, 0, None) == 1
+    assert b"backward version must be 1 to 6" in lib.fhoad_last_error()
+    assert lib.fhoad_forward_laplacian_backward(None, None, None, None, None, None, None, 0, -3, 6, None) == 2
+
+
+def test_torch_extension_reports_contract_errors_on_cpu() -> None:
+    from fused_hoad import _C
+
+    x = torch.zeros(4, 2)
+    p = torch.zeros(12737)
+    with pytest.raises(RuntimeError, match="version must be 0 to 5"):
+        _C.fused_forward_laplacian(x, p, 6)
+    with pytest.raises(RuntimeError, match="backward version must be 1 to 6"):
+        _C.fused_forward_laplacian_backward(x, p, x[:, 0], x[:, 0], 7)
+    with pytest.raises(RuntimeError, match="coordinates must be a CUDA tensor"):
+        _C.fused_forward_laplacian(x, p)
+
+
+@pytest.mark.gpu
+def test_raw_entry_points_match_the_torch_extension() -> None:
+    from gpu_helpers import announce, coordinates, packed, require_gpu_extension, upstream
+
+    require_gpu_extension()
+    announce("C ABI via ctypes vs fused_hoad._C, batch=5000")
+    from fused_hoad import _C
+
+    lib = _lib()
+    batch = 5000
+    p = packed(0)
+    x = coordinates(batch, seed=9)
+    gu, gl = upstream(batch, seed=9)
+    gu, gl = gu.reshape(-1).contiguous(), gl.reshape(-1).contiguous()
+    stream = torch.cuda.current_stream().cuda_stream
+    u = torch.empty(batch, 1, device="cuda")
+    lap = torch.empty(batch, 1, device="cuda")
+    status = lib.fhoad_forward_laplacian(x.data_ptr(), p.data_ptr(), u.data_ptr(), lap.data_ptr(), batch, 2, stream)
+    assert status == 0, lib.fhoad_last_error()
+    eu, el = _C.fused_forward_laplacian(x, p)
+    torch.cuda.synchronize()
+    assert torch.equal(u, eu) and torch.equal(lap, el)
+
+    ws_bytes = lib.fhoad_backward_workspace_size(batch)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    gp = torch.empty(12737, device="cuda")
+    gx = torch.empty(batch, 2, device="cuda")
+    status = lib.fhoad_forward_laplacian_backward(
+        x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), gp.data_ptr(), gx.data_ptr(),
+        ws.data_ptr(), ws_bytes, batch, 6, stream)
+    assert status == 0, lib.fhoad_last_error()
+    ep, ex = _C.fused_forward_laplacian_backward(x, p, gu, gl)
+    torch.cuda.synchronize()
+    assert torch.equal(gp, ep) and torch.equal(gx, ex)
+    # a workspace one byte short is refused
+    status = lib.fhoad_forward_laplacian_backward(
+        x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), gp.data_ptr(), gx.data_ptr(),
+        ws.data_ptr(), ws_bytes - 1, batch, 6, stream)
+    assert status == 4

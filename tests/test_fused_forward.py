@@ -1,0 +1,133 @@
+"""GPU parity of the gfx950 forward kernel (through fused_hoad._C and the C ABI).
+
+Tolerances: against the PyTorch forward Laplacian in FP32 (oracle/torch_ref.py, the
+reference's forward_laplacian.py restated) atol 1e-5 / rtol 1e-4, the north star's bar and
+the reference's test_fused.py:27-35; against the float64 oracle with saturating weights
+max |error| <= 1e-4 max |expected| (test_fused.py:38-49).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from golden_cases import CASE_NAMES, load_case
+from gpu_helpers import announce, coordinates, packed, require_gpu_extension, to_numpy64
+from oracle import jet, torch_ref
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _extension():
+    return require_gpu_extension()
+
+
+def _fused(x, p, version=2):
+    from fused_hoad import fused_forward_laplacian
+
+    return fused_forward_laplacian(x, p, version)
+
+
+# the reference's tile edges (test_fused.py:28) plus this kernel's: 16-point wave tiles
+@pytest.mark.parametrize(
+    "batch", [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 4097, 16384, 65536]
+)
+def test_forward_matches_torch_forward_laplacian(batch: int) -> None:
+    announce(f"forward vs torch forward Laplacian, batch={batch}")
+    p = packed(0)
+    x = coordinates(batch, seed=batch)
+    eu, el = torch_ref.forward_laplacian(p, x)
+    u, lap = _fused(x, p)
+    assert u.shape == lap.shape == (batch, 1)
+    torch.testing.assert_close(u, eu, atol=1e-5, rtol=1e-4)
+    torch.testing.assert_close(lap, el, atol=1e-5, rtol=1e-4)
+
+
+def test_forward_matches_float64_oracle_with_saturated_tanh() -> None:
+    announce("forward vs float64 oracle, weights x3, batch=4096")
+    p = packed(1, 3.0)
+    x = coordinates(4096, seed=1)
+    eu, el = jet.forward(to_numpy64(p), to_numpy64(x))
+    u, lap = _fused(x, p)
+    for got, want in ((u, eu), (lap, el)):
+        err = np.abs(to_numpy64(got).ravel() - want).max()
+        assert err <= 1e-4 * np.abs(want).max(), err
+
+
+@pytest.mark.parametrize("name", CASE_NAMES)
+def test_forward_matches_golden_fixture(name: str) -> None:
+    announce(f"forward vs golden fixture {name}")
+    case = load_case(name)
+    p = torch.from_numpy(case["parameters"]).cuda()
+    x = torch.from_numpy(case["coordinates"]).cuda()
+    u, lap = _fused(x, p)
+    np.testing.assert_allclose(to_numpy64(u).ravel(), case["u"], atol=1e-5, rtol=1e-4)
+    np.testing.assert_allclose(to_numpy64(lap).ravel(), case["laplacian"], atol=1e-5, rtol=1e-4)
+
+
+def test_forward_large_batch_matches_torch() -> None:
+    announce("forward vs torch forward Laplacian, batch=1048576")
+    p = packed(0)
+    x = coordinates(1 << 20, seed=3)
+    u, lap = _fused(x, p)
+    eu, el = torch_ref.forward_laplacian(p, x)
+    torch.testing.assert_close(u, eu, atol=1e-5, rtol=1e-4)
+    torch.testing.assert_close(lap, el, atol=1e-5, rtol=1e-4)
+
+
+def test_forward_is_bitwise_reproducible_and_version_independent() -> None:
+    announce("forward determinism and versions 0..5, batch=65536")
+    p = packed(0)
+    x = coordinates(65536, seed=5)
+    first = _fused(x, p)
+    for version in range(6):
+        again = _fused(x, p, version)
+        assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
+
+
+def test_forward_handles_empty_batch() -> None:
+    announce("forward, empty batch")
+    u, lap = _fused(torch.empty(0, 2, device="cuda"), packed(0))
+    assert u.shape == lap.shape == (0, 1)
+
+
+@pytest.mark.parametrize(
+    ("make", "message"),
+    [
+        (lambda: torch.zeros(4, 2, device="cuda", dtype=torch.float64), "float32"),
+        (lambda: torch.zeros(4, 3, device="cuda"), r"\[batch, 2\]"),
+        (lambda: torch.zeros(4, 2), "CUDA"),
+        (lambda: torch.zeros(2, 4, device="cuda").t(), "contiguous"),
+    ],
+)
+def test_forward_rejects_invalid_coordinates(make, message: str) -> None:
+    announce(f"forward rejects invalid coordinates ({message})")
+    with pytest.raises(RuntimeError, match=message):
+        _fused(make(), packed(0))
+
+
+def test_forward_rejects_bad_parameters_and_version() -> None:
+    announce("forward rejects bad parameters / version")
+    x = torch.zeros(4, 2, device="cuda")
+    with pytest.raises(RuntimeError, match="version"):
+        _fused(x, packed(0), 7)
+    with pytest.raises(RuntimeError, match=r"\[12737\]"):
+        _fused(x, torch.zeros(12736, device="cuda"))
+
+
+def test_backend_repacks_after_in_place_weight_update() -> None:
+    announce("fused_cuda backend repacks after an in-place update")
+    from fused_hoad import DEFAULT_POISSON_MLP, build_mlp, forward_laplacian, get_backend
+
+    torch.manual_seed(0)
+    model = build_mlp(DEFAULT_POISSON_MLP).cuda().requires_grad_(False)
+    x = coordinates(256, seed=8)
+    run = get_backend("fused_cuda")
+    run(model, x)
+    with torch.no_grad():
+        model[0].weight.mul_(0.5)
+    _, lap = run(model, x)
+    _, expected = forward_laplacian(model, x)
+    torch.testing.assert_close(lap, expected, atol=1e-5, rtol=1e-4)

@@ -1,0 +1,151 @@
+"""The fused kernels inside PyTorch training (autograd.Function, pack cache, Adam, graph
+capture), as in the reference's test_fused.py:98-159 and 233-262, plus the large-batch
+training config (262,144 points, 100 Adam steps, deterministic gradients)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_helpers import announce, coordinates, require_gpu_extension
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _extension():
+    return require_gpu_extension()
+
+
+def _model(seed: int = 0):
+    from fused_hoad import DEFAULT_POISSON_MLP, build_mlp
+
+    torch.manual_seed(seed)
+    return build_mlp(DEFAULT_POISSON_MLP).cuda()
+
+
+def _poisson_loss(u, lap, x):
+    from fused_hoad import manufactured_source
+
+    return (lap - manufactured_source(x)).pow(2).mean() + 0.1 * u.pow(2).mean()
+
+
+@pytest.mark.parametrize(
+    "name",
+    ["fused_cuda_v0", "fused_cuda_v1", "fused_cuda", "fused_cuda_bwd_v1", "fused_cuda_bwd_v3",
+     "fused_cuda_bwd_v5", "fused_cuda_bwd_v4", "fused_cuda_bwd_v2", "fused_cuda_recompute"],
+)
+def test_fused_gradients_match_forward_laplacian(name: str) -> None:
+    announce(f"full-loss gradients through autograd, backend={name}")
+    from fused_hoad import forward_laplacian, get_backend
+
+    model = _model()
+    x0 = coordinates(4096, seed=1)
+
+    def gradients(run):
+        model.zero_grad()
+        x = x0.clone().requires_grad_(True)
+        _poisson_loss(*run(model, x), x0).backward()
+        return [p.grad.clone() for p in model.parameters()] + [x.grad.clone()]
+
+    expected = gradients(forward_laplacian)
+    actual = gradients(get_backend(name))
+    for got, want in zip(actual, expected, strict=True):
+        torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-4)
+
+
+def test_fused_trains_like_forward_laplacian() -> None:
+    announce("50 Adam steps, fused vs forward_laplacian, batch=2048")
+    from fused_hoad import forward_laplacian, get_backend
+
+    x = coordinates(2048, seed=2)
+
+    def train(run):
+        model = _model()
+        opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+        losses = []
+        for _ in range(50):
+            opt.zero_grad()
+            loss = _poisson_loss(*run(model, x), x)
+            loss.backward()
+            opt.step()
+            losses.append(loss.item())
+        return losses
+
+    fused = train(get_backend("fused_cuda"))
+    reference = train(forward_laplacian)
+    assert fused[-1] < 0.5 * fused[0]
+    torch.testing.assert_close(torch.tensor(fused), torch.tensor(reference), rtol=1e-3, atol=0)
+
+
+def test_inference_path_stays_out_of_autograd() -> None:
+    announce("no_grad fused call")
+    from fused_hoad import get_backend
+
+    model = _model()
+    with torch.no_grad():
+        u, lap = get_backend("fused_cuda")(model, torch.zeros(8, 2, device="cuda"))
+    assert not u.requires_grad and not lap.requires_grad
+
+
+def test_graph_captured_training_step_matches_eager_step() -> None:
+    announce("whole-step graph capture vs eager steps, batch=2048")
+    from fused_hoad import get_backend
+    from fused_hoad.training import cuda_graph_step
+
+    x = coordinates(2048, seed=3)
+    run = get_backend("fused_cuda")
+
+    def train(graph: bool):
+        model = _model()
+        opt = torch.optim.Adam(model.parameters(), lr=1e-3, capturable=graph)
+
+        def loss_fn():
+            return _poisson_loss(*run(model, x), x)
+
+        if graph:
+            step = cuda_graph_step(loss_fn, opt, warmup=3)
+            return [step().item() for _ in range(20)]  # every replay checked, host sync between
+        losses = []
+        for _ in range(23):
+            opt.zero_grad(set_to_none=True)
+            loss = loss_fn()
+            loss.backward()
+            opt.step()
+            losses.append(loss.item())
+        return losses[3:]
+
+    torch.testing.assert_close(torch.tensor(train(True)), torch.tensor(train(False)), rtol=1e-4, atol=0)
+
+
+def _poisson_step_losses(batch: int, steps: int, backward: str):
+    from fused_hoad import manufactured_source
+    from fused_hoad.backends.fused import fused_laplacian
+
+    model = _model()
+    opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+    x = coordinates(batch, seed=7)
+    f = manufactured_source(x)
+    losses, first_grads = [], None
+    for step in range(steps):
+        opt.zero_grad(set_to_none=True)
+        _, lap = fused_laplacian(model, x, backward=backward)
+        loss = (lap - f).pow(2).mean()
+        loss.backward()
+        if step == 0:
+            first_grads = [p.grad.clone() for p in model.parameters()]
+        opt.step()
+        losses.append(loss.item())
+    return losses, first_grads
+
+
+def test_large_batch_training_is_deterministic_and_tracks_recompute() -> None:
+    announce("262144 points, 100 Adam steps: determinism and loss curve vs recompute")
+    losses_a, grads_a = _poisson_step_losses(262144, 100, "cuda")
+    losses_b, grads_b = _poisson_step_losses(262144, 100, "cuda")
+    assert losses_a == losses_b
+    for a, b in zip(grads_a, grads_b, strict=True):
+        assert torch.equal(a, b)
+    reference, _ = _poisson_step_losses(262144, 100, "recompute")
+    assert losses_a[-1] < losses_a[0]
+    torch.testing.assert_close(torch.tensor(losses_a), torch.tensor(reference), rtol=1e-3, atol=0)
