@@ -1,0 +1,316 @@
+"""Benchmark of the fused forward-Laplacian path on one MI355X.
+
+Metric: residual points/s (u, Laplacian u) at 64K points plus train-step ms at
+64K points, FP32, 1 GPU. One "step" is one fused residual evaluation of 65,536 points
+(coordinates already in HBM); the training step (fused forward + loss + fused backward + Adam
+lr 1e-3 on mean((Laplacian u - f)^2), f = -2 pi^2 sin(pi x) sin(pi y)) is timed the same way at
+65,536 points and reported as ``train_step_ms``.
+
+Correctness is checked before any timing: the fused forward against the package's PyTorch
+forward Laplacian (atol 1e-5 / rtol 1e-4) and the fused backward against the PyTorch
+recompute backward (1e-4 of each gradient block's scale); a mismatch aborts.
+
+Prints human-readable lines to stderr and ONE JSON line to stdout.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "expanded-gpu-optimization_amd"))
+
+METRIC = "residual points/sec (u,Δu) at 64K + train-step ms at 64K, FP32, 1 GPU"
+PEAK_FP32_MATRIX_TFLOPS = 157.3  # MI355X dense FP32 MFMA (256 CUs x 256 FLOP/clk x 2.4 GHz)
+FLOP_PER_POINT_FORWARD = 3 * 64 * 64 * 4 * 2  # hidden-layer contractions: 98,304
+FLOP_PER_POINT_BACKWARD = 2 * FLOP_PER_POINT_FORWARD  # dW + hbar (recompute not counted)
+REFERENCE_A5000 = {"residual_points_per_s_64k": 121.9e6, "train_step_ms_64k": 3.334,
+                   "hardware": "RTX A5000", "source": "reference results/2026-11-06-RTX-A5000-8454035"}
+TRAFFIC_FILE = ROOT / "profiles" / "forward_kernel_65536_traffic.json"
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def _parse() -> argparse.Namespace:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--points", type=int, default=65536)
+    parser.add_argument("--train-points", type=int, default=65536)
+    parser.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--calibrate-copy-mib", type=int, default=0,
+                        help="also run a plain device copy of this many MiB (rocprof counter scale)")
+    args = parser.parse_args()
+    if args.steps < 1 or args.warmup < 0 or args.points < 1 or args.train_points < 1:
+        parser.error("steps and points must be positive, warmup non-negative")
+    return args
+
+
+def _gpu_clock_mhz() -> float | None:
+    """Active shader-clock level from the amdgpu sysfs table (the line marked '*'), best
+    effort and without starting any process."""
+    for table in sorted(Path("/sys/class/drm").glob("card*/device/pp_dpm_sclk")):
+        try:
+            for line in table.read_text().splitlines():
+                if line.rstrip().endswith("*"):
+                    return float(line.split(":", 1)[1].strip().lower().split("mhz")[0])
+        except (OSError, ValueError, IndexError):
+            continue
+    return None
+
+
+def _events_timed(fn, iterations: int, torch):
+    """Run fn `iterations` times bracketed by synchronize; per-call HIP events on the current
+    stream (the stream the kernels are launched on). Returns (total_ms, per_call_ms list)."""
+    stream = torch.cuda.current_stream()
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iterations)]
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for begin, end in pairs:
+        begin.record(stream)
+        fn()
+        end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = (time.perf_counter() - start) * 1e3
+    return total_ms, [b.elapsed_time(e) for b, e in pairs]
+
+
+def _scaled_error(actual, expected) -> float:
+    return float((actual - expected).abs().max() / expected.abs().max().clamp_min(1e-30))
+
+
+def main() -> None:
+    args = _parse()
+    if args.gpus != 1:
+        log(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the path is data-parallel "
+            "over points and its multi-GPU design is described, not run. Use --gpus 1.")
+        sys.exit(2)
+
+    import torch
+
+    from fused_hoad import DEFAULT_POISSON_MLP, build_mlp, forward_laplacian, manufactured_source
+    from fused_hoad._extension import (
+        fused_forward_laplacian,
+        fused_forward_laplacian_backward,
+        load_extension,
+    )
+    from fused_hoad.backends.fused import _recompute_backward, fused_laplacian
+    from fused_hoad.parameters import pack_poisson_parameters
+
+    load_extension()  # fail loudly if the HIP extension is missing
+    if not torch.cuda.is_available():
+        raise SystemExit("no GPU visible")
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    props = torch.cuda.get_device_properties(device)
+    log(f"device: {props.name} ({getattr(props, 'gcnArchName', '?')}), CUs={props.multi_processor_count}, "
+        f"torch {torch.__version__}, hip {torch.version.hip}")
+
+    # ---- inputs: seeded model, coordinates U[-1,1]^2 from a seeded CPU generator ----
+    torch.manual_seed(0)
+    model = build_mlp(DEFAULT_POISSON_MLP).to(device)
+    params = pack_poisson_parameters(model)
+    gen = torch.Generator().manual_seed(0)
+    x = (torch.rand(args.points, 2, generator=gen) * 2 - 1).to(device)
+    x_train = (torch.rand(args.train_points, 2, generator=gen) * 2 - 1).to(device)
+
+    # ---- correctness before timing ----
+    with torch.no_grad():
+        u, lap = fused_forward_laplacian(x, params)
+        eu, el = forward_laplacian(model, x)
+    torch.testing.assert_close(u, eu, atol=1e-5, rtol=1e-4)
+    torch.testing.assert_close(lap, el, atol=1e-5, rtol=1e-4)
+    gu = torch.zeros(args.train_points, 1, device=device)
+    gl = torch.randn(args.train_points, 1, device=device, generator=torch.Generator(device=device).manual_seed(1))
+    gp, gx = fused_forward_laplacian_backward(x_train, params, gu, gl)
+    ex, ep = _recompute_backward(x_train, params, gu, gl, True, True)
+    bwd_err = max(_scaled_error(gp, ep), _scaled_error(gx, ex))
+    if bwd_err > 1e-4:
+        raise SystemExit(f"fused backward disagrees with the recompute backward: {bwd_err:.3e}")
+    log(f"check: forward within atol 1e-5/rtol 1e-4, backward max scaled error {bwd_err:.2e}")
+
+    # ---- residual: K fused forward calls ----
+    def residual_step():
+        fused_forward_laplacian(x, params)
+
+    for _ in range(args.warmup):
+        residual_step()
+    total_ms, per_call = _events_timed(residual_step, args.steps, torch)
+    ms_per_step = total_ms / args.steps
+    fwd_kernel_ms = statistics.mean(per_call)
+    points_per_s = args.points / (ms_per_step / 1e3)
+    log(f"residual {args.points} pts: {ms_per_step * 1e3:.1f} us/step wall, "
+        f"{fwd_kernel_ms * 1e3:.1f} us/call (events, mean), median {statistics.median(per_call) * 1e3:.1f} us, "
+        f"{points_per_s / 1e6:.1f} M points/s")
+
+    # ---- backward call alone (backward kernel + fixed-order reduction) ----
+    def backward_step():
+        fused_forward_laplacian_backward(x_train, params, gu, gl)
+
+    for _ in range(args.warmup):
+        backward_step()
+    _, bwd_calls = _events_timed(backward_step, args.steps, torch)
+    bwd_ms = statistics.mean(bwd_calls)
+
+    # ---- training step: fused forward + loss + fused backward + Adam ----
+    optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)
+    source = manufactured_source(x_train)
+
+    def train_step():
+        optimizer.zero_grad(set_to_none=True)
+        _, lap_t = fused_laplacian(model, x_train)
+        (lap_t - source).pow(2).mean().backward()
+        optimizer.step()
+
+    for _ in range(args.warmup):
+        train_step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(device)
+    baseline_bytes = torch.cuda.memory_allocated(device)
+    train_total_ms, train_calls = _events_timed(train_step, args.steps, torch)
+    train_ms = train_total_ms / args.steps
+    peak_mib = (torch.cuda.max_memory_allocated(device) - baseline_bytes) / 2**20
+    log(f"train step {args.train_points} pts: {train_ms:.3f} ms wall/step, "
+        f"median {statistics.median(train_calls):.3f} ms (events); backward call {bwd_ms * 1e3:.1f} us; "
+        f"peak {peak_mib:.1f} MiB above baseline")
+
+    if args.calibrate_copy_mib:
+        n = args.calibrate_copy_mib * 2**20 // 4
+        src = torch.ones(n, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration: copied {args.calibrate_copy_mib} MiB 5 times")
+
+    clock = _gpu_clock_mhz()
+    fwd_tflops = FLOP_PER_POINT_FORWARD * args.points / (fwd_kernel_ms / 1e3) / 1e12
+    bwd_tflops = FLOP_PER_POINT_BACKWARD * args.train_points / (bwd_ms / 1e3) / 1e12
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    roofline = {
+        "bound": "mfma",
+        "achieved": round(fwd_tflops, 3),
+        "peak": PEAK_FP32_MATRIX_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(fwd_tflops / PEAK_FP32_MATRIX_TFLOPS, 4),
+        "traffic": traffic,
+        "kernel": "forward_kernel",
+        "flop_per_launch": FLOP_PER_POINT_FORWARD * args.points,
+        "avg_launch_ms": round(fwd_kernel_ms, 5),
+    }
+    roofline_backward = {
+        "bound": "mfma",
+        "achieved": round(bwd_tflops, 3),
+        "peak": PEAK_FP32_MATRIX_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(bwd_tflops / PEAK_FP32_MATRIX_TFLOPS, 4),
+        "kernel": "backward_kernel + reduce_partials_kernel (one backward call)",
+        "flop_per_launch": FLOP_PER_POINT_BACKWARD * args.train_points,
+        "avg_launch_ms": round(bwd_ms, 5),
+    }
+    step_flop = (FLOP_PER_POINT_FORWARD + FLOP_PER_POINT_BACKWARD) * args.train_points
+    train_tflops = step_flop / (train_ms / 1e3) / 1e12
+
+    cpu_baseline = None
+    if not args.no_cpu_baseline:
+        cpu_baseline = _cpu_baseline(torch)
+
+    record = {
+        "metric": METRIC,
+        "value": round(points_per_s, 1),
+        "unit": "points/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (coordinates U[-1,1]^2 from a seeded CPU generator; torch.manual_seed(0) default nn.Linear init)",
+        "config": {
+            "workload": "fused residual (u, Laplacian u) of the 2->64x4->1 tanh MLP at 65,536 points; "
+                        "train step = fused forward + mean((Lap u - f)^2) + fused backward + Adam(lr 1e-3) at 65,536 points",
+            "points": args.points,
+            "train_points": args.train_points,
+        },
+        "train_step_ms": round(train_ms, 5),
+        "train_step_tflops": round(train_tflops, 3),
+        "train_step_peak_mib": round(peak_mib, 2),
+        "backward_call_ms": round(bwd_ms, 5),
+        "gpu_clock_mhz": clock,
+        "roofline": roofline,
+        "roofline_backward": roofline_backward,
+        "cpu_baseline": cpu_baseline,
+        "reference_published": REFERENCE_A5000,
+    }
+    print(json.dumps(record), flush=True)
+
+
+def _cpu_baseline(torch) -> dict:
+    """The reference's CPU path (oracle/torch_ref.py, a restatement of its PyTorch forward
+    Laplacian and eager-autograd training step) on this host's cores, on a bounded sample."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import torch_ref
+
+    threads = torch.get_num_threads()
+    model = torch_ref.reference_model(0)
+    flat = torch_ref.pack(model)
+    gen = torch.Generator().manual_seed(0)
+    x = torch.rand(65536, 2, generator=gen) * 2 - 1
+    x1k = x[:1024].contiguous()
+
+    def median_ms(fn, warmup, iterations):
+        for _ in range(warmup):
+            fn()
+        samples = []
+        for _ in range(iterations):
+            tick = time.perf_counter()
+            fn()
+            samples.append((time.perf_counter() - tick) * 1e3)
+        return statistics.median(samples)
+
+    with torch.no_grad():
+        res64k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x), 1, 5)
+        res1k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x1k), 3, 20)
+    optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)
+    source = torch_ref.poisson_source(x)
+    step_ms = median_ms(lambda: torch_ref.eager_train_step(model, x, source, optimizer), 1, 3)
+    cpu_model = "?"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    log(f"cpu baseline ({threads} threads, os.cpu_count()={os.cpu_count()}, {cpu_model}): "
+        f"forward Laplacian 64K {res64k_ms:.1f} ms, 1K {res1k_ms:.2f} ms; eager step 64K {step_ms:.1f} ms")
+    return {
+        "value": round(65536 / (res64k_ms / 1e3), 1),
+        "unit": "points/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": "oracle/torch_ref.py PyTorch forward Laplacian (u, Lap u) at 65,536 points, median of 5 calls "
+                  f"after 1 warmup ({res64k_ms:.1f} ms/call); 1,024 points: {res1k_ms:.2f} ms/call (median of 20); "
+                  f"eager nested-autograd + Adam train step at 65,536 points: {step_ms:.1f} ms/step (median of 3)",
+        "train_step_ms": round(step_ms, 3),
+        "residual_1k_ms": round(res1k_ms, 4),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": cpu_model,
+    }
+
+
+if __name__ == "__main__":
+    main()
