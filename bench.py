@@ -47,6 +47,9 @@ def _parse() -> argparse.Namespace:
     parser.add_argument("--points", type=int, default=65536)
     parser.add_argument("--train-points", type=int, default=65536)
     parser.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--kernels-only", action="store_true",
+                        help="after the correctness check, time only the fused forward and backward "
+                             "calls (for counter collection); prints no JSON line")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also run a plain device copy of this many MiB (rocprof counter scale)")
     args = parser.parse_args()
@@ -160,6 +163,10 @@ def main() -> None:
         backward_step()
     _, bwd_calls = _events_timed(backward_step, args.steps, torch)
     bwd_ms = statistics.mean(bwd_calls)
+
+    if args.kernels_only:
+        log(f"backward call {args.train_points} pts: {bwd_ms * 1e3:.1f} us (events, mean)")
+        return
 
     # ---- training step: fused forward + loss + fused backward + Adam ----
     optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)

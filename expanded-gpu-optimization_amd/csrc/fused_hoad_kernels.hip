@@ -21,11 +21,20 @@
 // is already in the operand layout of the next layer, and the tanh-jet update (which needs the
 // 4 components of one (neuron, point)) is local to a lane. Only the weights come from LDS.
 //
-// LDS weight layout. W[o][i] of a hidden layer is stored at 68 o - 3 (o & 3) + i (rows of 64
-// with a per-row skew). The forward reads W[16 mb + m][16 ob + 4 g + j] (lane part
-// 68 m - 3 (m & 3) + 4 g) and the backward's transposed product reads
-// W[16 ob + 4 g + j][16 ib + m] (lane part 272 g + m). Both lane parts hit 64 distinct banks
-// (mod 64) and the rest of each address is a compile-time immediate.
+// Scaled jet. Kernels carry (c v, J0, J1, lambda L) with c = -2 log2(e) and lambda = log2(e),
+// and pre-activations scaled the same way (the value bias is staged as c b). Then
+// exp(-2 |z_v|) is exp2(-|c z_v|) with no multiply, the value output c tanh(z_v) comes out of
+// one fma, and the Laplacian update is L' = s (z_L' + v' q) with v' = c tanh z_v (because
+// -2 lambda = c). w_out is staged as w_out / c and w_out / lambda for u and lap. Products of a
+// primal and its adjoint are scale-invariant, so dW and W^T zbar need no correction; bias
+// and layer-0 gradients pick up one factor c. FP32 MFMA runs on the same SIMD issue slots as
+// VALU work on gfx950 (measured: they do not co-execute), so every VALU instruction saved in
+// the jet update is MFMA time recovered.
+//
+// LDS weight layouts. The forward kernel keeps W in MFMA operand order (one 16-byte read per
+// k-step, see stage_operand_weights). The backward needs both W and W^T operands from one copy:
+// W[o][i] at 68 o + i, read as W[16 mb + m][16 ob + 4 g + j], j = 0..3 (16 bytes) for the forward
+// recompute and as W[16 ob + 4 g + j][16 ib + m] (4 bytes) for W^T zbar.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -44,19 +53,33 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 constexpr int kTile = 16;     // points per wave tile (the MFMA N dimension)
-constexpr int kWRow = 68;     // skewed LDS row pitch, see the header comment
-constexpr int kPlane = 4352;  // floats per skewed 64x64 plane (>= 68*63 - 9 + 64, multiple of 64)
+constexpr int kWRow = 68;     // LDS row pitch of the backward's 64-wide rows
+constexpr int kPlane = 4352;  // floats per 64 x 68 LDS plane
 
-// Small parameter blocks mirrored in LDS (float offsets inside s_small).
-constexpr int kSmallW0 = 0;                                  // W0[64][2]
-constexpr int kSmallB0 = kSmallW0 + kHidden * kInputs;        // b0[64]
-constexpr int kSmallBh = kSmallB0 + kHidden;                  // b1..b3, [3][64]
-constexpr int kSmallWout = kSmallBh + 3 * kHidden;            // w_out[64]
-constexpr int kSmallBout = kSmallWout + kHidden;              // b_out
+// Scale factors of the carried jet (see the header comment).
+constexpr float kC = -2.8853900817779268f;       // c = -2 log2(e)
+constexpr float kAbsC = 2.8853900817779268f;     // |c|
+constexpr float kLambda = 1.4426950408889634f;   // lambda = log2(e)
+constexpr float kKappa = -0.24022650695910071f;  // -2 / c^2
+
+// Small parameter blocks in LDS (float offsets inside s_small), each [64] over neurons.
+constexpr int kSmallCwx = 0;                       // c W0[:, 0]
+constexpr int kSmallCwy = kSmallCwx + kHidden;     // c W0[:, 1]
+constexpr int kSmallCb0 = kSmallCwy + kHidden;     // c b0
+constexpr int kSmallWx = kSmallCb0 + kHidden;      // W0[:, 0]
+constexpr int kSmallWy = kSmallWx + kHidden;       // W0[:, 1]
+constexpr int kSmallQ0 = kSmallWy + kHidden;       // W0[:, 0]^2 + W0[:, 1]^2
+constexpr int kSmallBh = kSmallQ0 + kHidden;       // c b1..b3, [3][64]
+constexpr int kSmallWoutV = kSmallBh + 3 * kHidden;  // w_out / c
+constexpr int kSmallWoutL = kSmallWoutV + kHidden;   // w_out / lambda
+constexpr int kSmallBout = kSmallWoutL + kHidden;    // b_out
 constexpr int kSmallFloats = kSmallBout + 4;
 
-// Lane-dependent parts of the two LDS access patterns.
-__device__ __forceinline__ int lane_rows(int m, int g) { return kWRow * m - 3 * (m & 3) + 4 * g; }
+// Lane-dependent parts of the backward's two LDS access patterns on pitch-68 planes (value
+// (row, col) at 68 row + col): reading 4 consecutive columns of row m (16 bytes at
+// 68 m + 4 g) and reading one column m of rows 4 g + j (4 bytes at 272 g + m + 68 j). In both,
+// the 64 lanes cover distinct banks per 16-lane group, and the remaining offsets are immediates.
+__device__ __forceinline__ int lane_rows(int m, int g) { return kWRow * m + 4 * g; }
 __device__ __forceinline__ int lane_cols(int m, int g) { return 272 * g + m; }
 
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
@@ -65,112 +88,215 @@ __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
 
 __device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
-// tanh and its derivative from t = exp(-2|z|), with r = 1 / (1 + t):
-//   |tanh z| = (1 - t) r,   s = 1 - tanh^2 z = 4 t r^2.
-// Written from the identity tanh z = (1 - e^{-2z}) / (1 + e^{-2z}) on v_exp_f32 / v_rcp_f32.
-// s is formed without the 1 - a^2 cancellation, so it keeps full relative accuracy when tanh
-// saturates; t flushes to 0 for |z| > ~44, giving a = +-1, s = 0.
-__device__ __forceinline__ void tanh_and_slope(float z, float& a, float& s) {
-  constexpr float kMinusTwoLog2e = -2.8853900817779268f;  // -2 / ln 2
-  const float t = __builtin_amdgcn_exp2f(kMinusTwoLog2e * __builtin_fabsf(z));
-  const float r = __builtin_amdgcn_rcpf(1.0f + t);
-  a = __builtin_copysignf((1.0f - t) * r, z);
-  s = (4.0f * t) * (r * r);
+// tanh in the scaled jet. Input zv = c z_v; outputs v = c tanh(z_v) and s = 1 - tanh^2 z_v.
+// With t = exp(-2|z_v|) = exp2(-|zv|) and u = 2 / (1 + t) = 1 + |tanh z_v|:
+//   1 - |tanh z_v| = t u,   s = (1 + |tanh|)(1 - |tanh|) = u (t u),
+//   |v| = |c| (1 - t u),    sign(v) = sign(c z_v) = sign(zv).
+// Derived from tanh z = (1 - e^{-2z}) / (1 + e^{-2z}) on v_exp_f32 / v_rcp_f32; s has no
+// 1 - a^2 cancellation, so it keeps its relative accuracy where tanh saturates, and t flushes to
+// 0 for |z_v| > ~44 (tanh = +-1, s = 0). 5 VALU + 2 transcendental instructions.
+__device__ __forceinline__ void tanh_scaled(float zv, float& v, float& s) {
+  const float t = __builtin_amdgcn_exp2f(-__builtin_fabsf(zv));
+  const float u = __builtin_amdgcn_rcpf(__builtin_fmaf(t, 0.5f, 0.5f));
+  const float w = t * u;
+  s = u * w;
+  v = __builtin_copysignf(__builtin_fmaf(w, -kAbsC, kAbsC), zv);
 }
 
-// Forward tanh jet: (z_v, z_J0, z_J1, z_L) -> (v, J0, J1, L).
+// Forward tanh jet in scaled variables: (c z_v, z_J0, z_J1, lambda z_L) ->
+// (c v, J0, J1, lambda L) with v = tanh z_v, J = s z_J, L = s z_L - 2 v s q, q = |z_J|^2.
 __device__ __forceinline__ void tanh_jet(float zv, float zj0, float zj1, float zl, float& v,
                                          float& j0, float& j1, float& l) {
-  float a, s;
-  tanh_and_slope(zv, a, s);
+  float s;
+  tanh_scaled(zv, v, s);
   const float q = __builtin_fmaf(zj0, zj0, zj1 * zj1);
-  v = a;
   j0 = s * zj0;
   j1 = s * zj1;
-  l = __builtin_fmaf(-2.0f * a * s, q, s * zl);
+  l = s * __builtin_fmaf(v, q, zl);
 }
 
-// Adjoint of the tanh jet (/root/reference/csrc/fused_backward.cu:29-33), with s2 = -2 a s,
-// s3 = 2 s (2 a^2 - s), q = z_J0^2 + z_J1^2:
-//   zbar_v  = vbar s + (Jbar . z_J) s2 + Lbar (z_L s2 + q s3)
-//   zbar_Jd = Jbar_d s + 2 Lbar s2 z_Jd
-//   zbar_L  = Lbar s
-// The adjoint (vbar, J0bar, J1bar, Lbar) is replaced by zbar in place.
-__device__ __forceinline__ void tanh_jet_adjoint(float zv, float zj0, float zj1, float zl,
-                                                 float& bv, float& bj0, float& bj1, float& bl) {
-  float a, s;
-  tanh_and_slope(zv, a, s);
-  const float s2 = -2.0f * a * s;
-  const float s3 = 2.0f * s * __builtin_fmaf(2.0f * a, a, -s);
+// Adjoint of tanh_jet in the same scaled variables (the adjoint of a scaled quantity is the
+// unscaled adjoint divided by the scale). With v' = c tanh z_v, P = z_L' + v' q and
+// kappa = -2 / c^2 (so d s / d(c z_v) = kappa v' s):
+//   zbar_v' = s [vbar' + kappa v' (Jbar . z_J) + Lbar' (kappa v' P + s q)]
+//   zbar_Jd = s (Jbar_d + 2 Lbar' v' z_Jd)
+//   zbar_L' = s Lbar'
+// This is the reference's tanh_backward (/root/reference/csrc/fused_backward.cu:29-33, 75-89)
+// rewritten for the scaled jet. The adjoint (vbar', J0bar, J1bar, Lbar') is replaced in place.
+__device__ __forceinline__ void tanh_jet_adjoint_vs(float v, float s, float zj0, float zj1,
+                                                    float zl, float& bv, float& bj0, float& bj1,
+                                                    float& bl) {
   const float q = __builtin_fmaf(zj0, zj0, zj1 * zj1);
   const float dot = __builtin_fmaf(bj0, zj0, bj1 * zj1);
-  const float curv = __builtin_fmaf(zl, s2, q * s3);
-  const float lb2 = 2.0f * bl * s2;
-  const float nv = __builtin_fmaf(bv, s, __builtin_fmaf(dot, s2, bl * curv));
-  const float nj0 = __builtin_fmaf(bj0, s, lb2 * zj0);
-  const float nj1 = __builtin_fmaf(bj1, s, lb2 * zj1);
+  const float p = __builtin_fmaf(v, q, zl);
+  const float kv = kKappa * v;
+  const float t1 = __builtin_fmaf(kv, dot, bv);
+  const float t2 = __builtin_fmaf(kv, p, s * q);
+  const float nv = s * __builtin_fmaf(bl, t2, t1);
+  const float lbv = 2.0f * bl * v;
+  bj0 = s * __builtin_fmaf(lbv, zj0, bj0);
+  bj1 = s * __builtin_fmaf(lbv, zj1, bj1);
   bv = nv;
-  bj0 = nj0;
-  bj1 = nj1;
-  bl = bl * s;
+  bl = s * bl;
 }
 
-// Copy the packed parameters into LDS: the three hidden W into skewed planes, the small
-// blocks (W0, biases, w_out, b_out) verbatim. Reads are coalesced 4-byte loads, so the
-// parameter buffer needs no particular alignment.
-__device__ __forceinline__ void stage_parameters(const float* __restrict__ params, float* s_w,
-                                                 float* s_small, int tid, int threads) {
-  for (int k = tid; k < 3 * kHidden * kHidden; k += threads) {
-    const int layer = k >> 12;
-    const int o = (k >> 6) & 63;
-    const int i = k & 63;
-    s_w[layer * kPlane + kWRow * o - 3 * (o & 3) + i] =
-        params[kHiddenBase + layer * kHiddenStride + (o << 6) + i];
-  }
-  for (int k = tid; k < kHidden * kInputs + kHidden; k += threads) {
-    s_small[kSmallW0 + k] = params[k];  // W0 then b0 are contiguous in the ABI
+__device__ __forceinline__ void tanh_jet_adjoint(float zv, float zj0, float zj1, float zl,
+                                                 float& bv, float& bj0, float& bj1, float& bl) {
+  float v, s;
+  tanh_scaled(zv, v, s);
+  tanh_jet_adjoint_vs(v, s, zj0, zj1, zl, bv, bj0, bj1, bl);
+}
+
+// Small-parameter staging shared by both kernels (see kSmallCwx for the scaled forms).
+__device__ __forceinline__ void stage_small(const float* __restrict__ params, float* s_small,
+                                            int tid, int threads) {
+  for (int o = tid; o < kHidden; o += threads) {
+    const float wx = params[kInputs * o];
+    const float wy = params[kInputs * o + 1];
+    s_small[kSmallCwx + o] = kC * wx;
+    s_small[kSmallCwy + o] = kC * wy;
+    s_small[kSmallCb0 + o] = kC * params[kLayer0Bias + o];
+    s_small[kSmallWx + o] = wx;
+    s_small[kSmallWy + o] = wy;
+    s_small[kSmallQ0 + o] = __builtin_fmaf(wx, wx, wy * wy);
+    const float wo = params[kOutputBase + o];
+    s_small[kSmallWoutV + o] = wo * (1.0f / kC);
+    s_small[kSmallWoutL + o] = wo * (1.0f / kLambda);
   }
   for (int k = tid; k < 3 * kHidden; k += threads) {
     const int layer = k >> 6;
-    s_small[kSmallBh + k] = params[kHiddenBase + layer * kHiddenStride + kHidden * kHidden + (k & 63)];
+    s_small[kSmallBh + k] =
+        kC * params[kHiddenBase + layer * kHiddenStride + kHidden * kHidden + (k & 63)];
   }
-  for (int k = tid; k < kHidden + 1; k += threads) {
-    s_small[kSmallWout + k] = params[kOutputBase + k];
+  if (tid == 0) s_small[kSmallBout] = params[kOutputBase + kHidden];
+}
+
+// Hidden-weight staging: every thread issues all of its global loads before its first LDS
+// write (16-byte loads when the parameter buffer is 16-byte aligned, 4-byte loads otherwise),
+// then scatters the values with put(layer, o, i, value) for W_layer[o][i].
+template <int kThreads, typename Put>
+__device__ __forceinline__ void stage_hidden(const float* __restrict__ params, int tid, Put put) {
+  constexpr int kQuads = 3 * kHidden * kHidden / 4;
+  constexpr int kPerThread = (kQuads + kThreads - 1) / kThreads;
+  if ((reinterpret_cast<uintptr_t>(params) & 15) == 0) {
+    f4 v[kPerThread];
+#pragma unroll
+    for (int n = 0; n < kPerThread; ++n) {
+      const int q = tid + n * kThreads;
+      if (q < kQuads) {
+        const int layer = q >> 10, o = (q >> 4) & 63, i = (q & 15) << 2;
+        v[n] = *reinterpret_cast<const f4*>(params + kHiddenBase + layer * kHiddenStride +
+                                            (o << 6) + i);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < kPerThread; ++n) {
+      const int q = tid + n * kThreads;
+      if (q < kQuads) {
+        const int layer = q >> 10, o = (q >> 4) & 63, i = (q & 15) << 2;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) put(layer, o, i + e, v[n][e]);
+      }
+    }
+  } else {
+    for (int k = tid; k < 4 * kQuads; k += kThreads) {
+      const int layer = k >> 12, o = (k >> 6) & 63, i = k & 63;
+      put(layer, o, i, params[kHiddenBase + layer * kHiddenStride + (o << 6) + i]);
+    }
   }
 }
 
-// Layer-0 weights of the 4 neurons o = 16 mb + 4 g + r (r = 0..3) held by this lane.
+// Copy the packed parameters into LDS for the backward: the three hidden W into pitch-68
+// planes, the small blocks in the scaled forms listed at kSmallCwx.
+template <int kThreads>
+__device__ __forceinline__ void stage_parameters(const float* __restrict__ params, float* s_w,
+                                                 float* s_small, int tid) {
+  stage_hidden<kThreads>(params, tid, [&](int layer, int o, int i, float value) {
+    s_w[layer * kPlane + kWRow * o + i] = value;
+  });
+  stage_small(params, s_small, tid, kThreads);
+}
+
+// Forward-only LDS layout of the hidden weights, in MFMA operand order: for hidden layer l,
+// k-step (ob, j) and lane (m, g), the 16 bytes at f4 index (16 l + 4 ob + j) * 64 + lane hold
+// W[16 mb + m][16 ob + 4 g + j] for mb = 0..3. One ds_read_b128 per k-step feeds the 4 MFMAs
+// of that step; the 64 lanes read 1 KB contiguously (no bank conflicts) and every k-step offset
+// is an instruction immediate.
+constexpr int kOperandLayerF4 = 16 * kWave;  // f4 entries per layer (16 KB)
+
+template <int kThreads>
+__device__ __forceinline__ void stage_operand_weights(const float* __restrict__ params, float* s_wa,
+                                                      int tid) {
+  stage_hidden<kThreads>(params, tid, [&](int layer, int o, int i, float value) {
+    const int mb = o >> 4, m = o & 15, ob = i >> 4, g = (i >> 2) & 3, j = i & 3;
+    s_wa[((layer * 16 + ob * 4 + j) * kWave + 16 * g + m) * 4 + mb] = value;
+  });
+}
+
+// Layer-0 data of the 4 neurons o = 16 mb + 4 g + r (r = 0..3) held by this lane.
 struct Layer0Weights {
-  f4 wx, wy, b;
+  f4 cwx, cwy, cb;  // scaled, for the pre-activation c z_v = c (W0 x + b0)
+  f4 wx, wy, q;     // z_J0, z_J1 of layer 0 (the W0 columns) and their squared norm
 };
 
 __device__ __forceinline__ Layer0Weights layer0_weights(const float* s_small, int mb, int g) {
   const int o = 16 * mb + 4 * g;
-  const f4 lo = lds4(s_small + kSmallW0 + 2 * o);
-  const f4 hi = lds4(s_small + kSmallW0 + 2 * o + 4);
   Layer0Weights w;
-  w.wx = f4{lo[0], lo[2], hi[0], hi[2]};
-  w.wy = f4{lo[1], lo[3], hi[1], hi[3]};
-  w.b = lds4(s_small + kSmallB0 + o);
+  w.cwx = lds4(s_small + kSmallCwx + o);
+  w.cwy = lds4(s_small + kSmallCwy + o);
+  w.cb = lds4(s_small + kSmallCb0 + o);
+  w.wx = lds4(s_small + kSmallWx + o);
+  w.wy = lds4(s_small + kSmallWy + o);
+  w.q = lds4(s_small + kSmallQ0 + o);
   return w;
 }
 
+__device__ __forceinline__ float layer0_zv(const Layer0Weights& w, int r, float x0, float x1) {
+  return __builtin_fmaf(w.cwx[r], x0, __builtin_fmaf(w.cwy[r], x1, w.cb[r]));
+}
+
 // Hidden-layer product acc[mb][c] += W[16 mb + ., :] H[:, c, .] with H in registers (see the
-// header comment for the k-step assignment). w points at this lane's row base in the layer's
-// LDS plane.
+// header comment for the k-step assignment), for the backward's forward recompute: w points at
+// this lane's row base (68 m + 4 g) in the layer's pitch-68 plane, and one 16-byte read gives
+// the A operands of k-steps (ob, 0..3). The first k-step takes its C operand from `bias`
+// (value component) or zero, so no accumulator needs initialising.
 __device__ __forceinline__ void hidden_product(const float* w, const f4 (&h)[4][4],
-                                               f4 (&acc)[4][4]) {
+                                               const f4 (&bias)[4], f4 (&acc)[4][4]) {
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) {
+    f4 a[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) a[mb] = lds4(w + 1088 * mb + 16 * ob);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f4 cin = (ob | j) ? acc[mb][c] : (c == 0 ? bias[mb] : f4{0.f, 0.f, 0.f, 0.f});
+          acc[mb][c] = mfma(a[mb][j], h[ob][c][j], cin);
+        }
+      }
+    }
+  }
+}
+
+// Forward hidden product with the operand-native weight layout: wa points at this lane's f4
+// in the layer's block; k-step (ob, j) reads wa[(4 ob + j) * 64].
+__device__ __forceinline__ void hidden_product_native(const f4* wa, const f4 (&h)[4][4],
+                                                      const f4 (&bias)[4], f4 (&acc)[4][4]) {
 #pragma unroll
   for (int ob = 0; ob < 4; ++ob) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float a[4];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) a[mb] = w[1088 * mb + 16 * ob + j];
+      const f4 a = wa[(4 * ob + j) * kWave];
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[mb][c] = mfma(a[mb], h[ob][c][j], acc[mb][c]);
+        for (int c = 0; c < 4; ++c) {
+          const f4 cin = (ob | j) ? acc[mb][c] : (c == 0 ? bias[mb] : f4{0.f, 0.f, 0.f, 0.f});
+          acc[mb][c] = mfma(a[mb], h[ob][c][j], cin);
+        }
       }
     }
   }
@@ -181,33 +307,36 @@ __device__ __forceinline__ void hidden_product(const float* w, const f4 (&h)[4][
 __device__ __forceinline__ void hidden_product_t(const float* w, const f4 (&zb)[4][4],
                                                  f4 (&hb)[4][4]) {
 #pragma unroll
-  for (int ib = 0; ib < 4; ++ib) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) hb[ib][c] = f4{0.f, 0.f, 0.f, 0.f};
-  }
-#pragma unroll
   for (int ob = 0; ob < 4; ++ob) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float a[4];
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) a[ib] = w[1088 * ob + 65 * j + 16 * ib];
+      for (int ib = 0; ib < 4; ++ib) a[ib] = w[1088 * ob + kWRow * j + 16 * ib];
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) hb[ib][c] = mfma(a[ib], zb[ob][c][j], hb[ib][c]);
+        for (int c = 0; c < 4; ++c) {
+          const f4 cin = (ob | j) ? hb[ib][c] : f4{0.f, 0.f, 0.f, 0.f};
+          hb[ib][c] = mfma(a[ib], zb[ob][c][j], cin);
+        }
       }
     }
   }
 }
 
-__device__ __forceinline__ void bias_init(const float* s_small, int layer, int g, f4 (&acc)[4][4]) {
+// Scaled value biases c b of the 4 x 4 neurons 16 mb + 4 g + r held by this lane.
+__device__ __forceinline__ void load_bias(const float* s_small, int layer, int g, f4 (&bias)[4]) {
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    acc[mb][0] = lds4(s_small + kSmallBh + layer * kHidden + 16 * mb + 4 * g);
-#pragma unroll
-    for (int c = 1; c < 4; ++c) acc[mb][c] = f4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int mb = 0; mb < 4; ++mb) bias[mb] = lds4(s_small + kSmallBh + layer * kHidden + 16 * mb + 4 * g);
+}
+
+// acc = W_layer h + bias, for hidden layer `layer` (0..2) with w at this lane's row base.
+__device__ __forceinline__ void hidden_layer(const float* s_small, const float* w_rows, int layer,
+                                             int g, const f4 (&h)[4][4], f4 (&acc)[4][4]) {
+  f4 bias[4];
+  load_bias(s_small, layer, g, bias);
+  hidden_product(w_rows + layer * kPlane, h, bias, acc);
 }
 
 __device__ __forceinline__ void apply_tanh_jet(const f4 (&z)[4][4], f4 (&h)[4][4]) {
@@ -225,7 +354,28 @@ __device__ __forceinline__ void apply_tanh_jet(const f4 (&z)[4][4], f4 (&h)[4][4
   }
 }
 
-// Layer 0 in closed form: the input jet is (x, I, 0), so z_J = W0 columns and z_L = 0.
+// apply_tanh_jet that also returns (v', s) of every value.
+__device__ __forceinline__ void apply_tanh_jet_vs(const f4 (&z)[4][4], f4 (&h)[4][4],
+                                                  f4 (&tv)[4], f4 (&ts)[4]) {
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v, sl;
+      tanh_scaled(z[mb][0][r], v, sl);
+      const float q = __builtin_fmaf(z[mb][1][r], z[mb][1][r], z[mb][2][r] * z[mb][2][r]);
+      h[mb][0][r] = v;
+      h[mb][1][r] = sl * z[mb][1][r];
+      h[mb][2][r] = sl * z[mb][2][r];
+      h[mb][3][r] = sl * __builtin_fmaf(v, q, z[mb][3][r]);
+      tv[mb][r] = v;
+      ts[mb][r] = sl;
+    }
+  }
+}
+
+// Layer 0 in closed form: the input jet is (x, I, 0), so z_J = W0 columns and z_L = 0, and
+// the tanh jet's q = |z_J|^2 is a per-neuron constant.
 __device__ __forceinline__ void layer0_forward(const float* s_small, int g, float x0, float x1,
                                                f4 (&h)[4][4]) {
 #pragma unroll
@@ -233,16 +383,21 @@ __device__ __forceinline__ void layer0_forward(const float* s_small, int g, floa
     const Layer0Weights w = layer0_weights(s_small, mb, g);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float zv = __builtin_fmaf(w.wx[r], x0, __builtin_fmaf(w.wy[r], x1, w.b[r]));
-      float v, j0, j1, l;
-      tanh_jet(zv, w.wx[r], w.wy[r], 0.0f, v, j0, j1, l);
+      float v, s;
+      tanh_scaled(layer0_zv(w, r, x0, x1), v, s);
       h[mb][0][r] = v;
-      h[mb][1][r] = j0;
-      h[mb][2][r] = j1;
-      h[mb][3][r] = l;
+      h[mb][1][r] = s * w.wx[r];
+      h[mb][2][r] = s * w.wy[r];
+      h[mb][3][r] = s * (v * w.q[r]);
     }
   }
 }
+
+// The small LDS parameters read per tile have loop-invariant addresses; left alone, the
+// compiler hoists those reads out of the tile loop and keeps ~100 values live in registers for
+// the whole kernel. An empty asm statement with a memory clobber at the top of each tile keeps
+// them as per-tile LDS reads.
+__device__ __forceinline__ void keep_lds_reads_in_loop() { __asm__ volatile("" ::: "memory"); }
 
 __device__ __forceinline__ float sum_lane_groups(float x) {
   x += __shfl_xor(x, 16);
@@ -260,20 +415,22 @@ __global__ void __launch_bounds__(kWaves * kWave)
 forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                float* __restrict__ output, float* __restrict__ laplacian, int64_t batch,
                int64_t tiles) {
-  __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
+  __shared__ __attribute__((aligned(16))) float s_wa[3 * kOperandLayerF4 * 4];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
-  stage_parameters(params, s_w, s_small, threadIdx.x, kWaves * kWave);
+  stage_operand_weights<kWaves * kWave>(params, s_wa, threadIdx.x);
+  stage_small(params, s_small, threadIdx.x, kWaves * kWave);
   __syncthreads();
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int m = lane & 15;
   const int g = lane >> 4;
-  const float* w_lane = s_w + lane_rows(m, g);
+  const f4* wa_lane = reinterpret_cast<const f4*>(s_wa) + lane;
   const int64_t step = static_cast<int64_t>(gridDim.x) * kWaves;
+  const int m = lane & 15;
 
   for (int64_t tile = blockIdx.x + static_cast<int64_t>(wave) * gridDim.x; tile < tiles;
        tile += step) {
+    keep_lds_reads_in_loop();
     const int64_t point = tile * kTile + m;
     const bool active = point < batch;
     float x0 = 0.0f, x1 = 0.0f;
@@ -284,19 +441,22 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
     f4 h[4][4];
     layer0_forward(s_small, g, x0, x1, h);
     for (int layer = 0; layer < 3; ++layer) {
+      f4 bias[4];
+      load_bias(s_small, layer, g, bias);
       f4 acc[4][4];
-      bias_init(s_small, layer, g, acc);
-      hidden_product(w_lane + layer * kPlane, h, acc);
+      hidden_product_native(wa_lane + layer * kOperandLayerF4, h, bias, acc);
       apply_tanh_jet(acc, h);
     }
+    // u = w_out . v + b_out and lap = w_out . L, from the scaled jet.
     float u = 0.0f, lap = 0.0f;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
-      const f4 w = lds4(s_small + kSmallWout + 16 * mb + 4 * g);
+      const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+      const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        u = __builtin_fmaf(w[r], h[mb][0][r], u);
-        lap = __builtin_fmaf(w[r], h[mb][3][r], lap);
+        u = __builtin_fmaf(wv[r], h[mb][0][r], u);
+        lap = __builtin_fmaf(wl[r], h[mb][3][r], lap);
       }
     }
     u = sum_lane_groups(u);
@@ -335,12 +495,13 @@ static_assert(kMaxSlots % kReduceGroups == 0, "reduction tree must tile the slot
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
-// Stage two jet components of this wave's zbar and h_prev into the dW staging buffer. Rows
-// are the workgroup tile's 64 points, columns the 64 neurons, same skewed pitch as weights.
-// zb components (c0, c0+1) go to planes 0, 1 and h_prev components to planes 2, 3.
+// Stage two jet components of this wave's zbar and h_prev into the dW staging buffer: planes
+// of [neuron][tile point] at pitch 68, so this lane's value of neuron 16 mb + 4 g + r at point
+// 16 w + m lands at stage_lane + 1088 mb + 68 r. zbar components go to planes 0, 1 and h_prev
+// components to planes 2, 3.
 __device__ __forceinline__ void stage_write(float* stage_lane, int mb, int r, float z_a,
                                             float z_b, float h_a, float h_b) {
-  float* p = stage_lane + 16 * mb + r;
+  float* p = stage_lane + 1088 * mb + kWRow * r;
   p[0] = z_a;
   p[kPlane] = z_b;
   p[2 * kPlane] = h_a;
@@ -348,24 +509,25 @@ __device__ __forceinline__ void stage_write(float* stage_lane, int mb, int r, fl
 }
 
 // dW[16 w + ., 16 nb + .] += sum over (2 staged components, 64 points) of zbar h_prev^T.
-// Lane (m, g) reads zbar[16 w + m][p] and h_prev[16 nb + m][p] for p = 16 s + 4 g + k, so the
-// MFMA contracts over points. Returns the sum of this lane's plane-0 zbar reads (the bias
-// gradient partial when plane 0 holds zbar_v).
-__device__ __forceinline__ float dw_product(const float* stage_cols, int w, f4 (&dw)[4]) {
+// Lane (m, g) reads zbar[16 w + m][p] and h_prev[16 nb + m][p] for p = 16 s + 4 g + k,
+// k = 0..3, as 16-byte reads (stage_rows = this lane's 68 m + 4 g), so the MFMA contracts over
+// points. Returns the sum of this lane's plane-0 zbar reads (the bias gradient partial when
+// plane 0 holds zbar_v).
+__device__ __forceinline__ float dw_product(const float* stage_rows, int w, f4 (&dw)[4]) {
   float bias = 0.0f;
 #pragma unroll
   for (int cc = 0; cc < 2; ++cc) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
+      const f4 a = lds4(stage_rows + cc * kPlane + 1088 * w + 16 * s);
+      f4 b[4];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) b[nb] = lds4(stage_rows + (2 + cc) * kPlane + 1088 * nb + 16 * s);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int off = cc * kPlane + 1088 * s + 65 * k;
-        const float a = stage_cols[off + 16 * w];
-        if (cc == 0) bias += a;
+        if (cc == 0) bias += a[k];
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          dw[nb] = mfma(a, stage_cols[off + 2 * kPlane + 16 * nb], dw[nb]);
-        }
+        for (int nb = 0; nb < 4; ++nb) dw[nb] = mfma(a[k], b[nb][k], dw[nb]);
       }
     }
   }
@@ -373,25 +535,27 @@ __device__ __forceinline__ float dw_product(const float* stage_cols, int w, f4 (
 }
 
 // Sum of staged plane `plane` over the 64 points for neuron 16 w + m, complete in every lane.
-__device__ __forceinline__ float plane_sum(const float* stage_cols, int plane, int w) {
+__device__ __forceinline__ float plane_sum(const float* stage_rows, int plane, int w) {
   float acc = 0.0f;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) acc += stage_cols[plane * kPlane + 1088 * s + 65 * k + 16 * w];
+    const f4 v = lds4(stage_rows + plane * kPlane + 1088 * w + 16 * s);
+    acc += (v[0] + v[1]) + (v[2] + v[3]);
   }
   return sum_lane_groups(acc);
 }
 
 // Replace a hidden layer's pre-activation z by its adjoint zbar, given the adjoint hb of the
-// layer's output (tanh-jet adjoint, lane-local).
-__device__ __forceinline__ void tanh_adjoint_in_place(f4 (&z)[4][4], const f4 (&hb)[4][4]) {
+// layer's output and the layer's (v', s) from tanh_scaled (lane-local).
+__device__ __forceinline__ void tanh_adjoint_in_place(f4 (&z)[4][4], const f4 (&hb)[4][4],
+                                                      const f4 (&tv)[4], const f4 (&ts)[4]) {
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float bv = hb[mb][0][r], bj0 = hb[mb][1][r], bj1 = hb[mb][2][r], bl = hb[mb][3][r];
-      tanh_jet_adjoint(z[mb][0][r], z[mb][1][r], z[mb][2][r], z[mb][3][r], bv, bj0, bj1, bl);
+      tanh_jet_adjoint_vs(tv[mb][r], ts[mb][r], z[mb][1][r], z[mb][2][r], z[mb][3][r], bv, bj0,
+                          bj1, bl);
       z[mb][0][r] = bv;
       z[mb][1][r] = bj0;
       z[mb][2][r] = bj1;
@@ -400,49 +564,56 @@ __device__ __forceinline__ void tanh_adjoint_in_place(f4 (&z)[4][4], const f4 (&
   }
 }
 
-// dW += zbar h_prev^T over the workgroup tile, in two passes of two jet components, where
-// h_prev = tanh_jet(zp) is rebuilt from the previous layer's pre-activation (or, with
-// kFromLayer0, from layer 0's closed form z = (W0 x + b0, W0[:,0], W0[:,1], 0)). Adds the
-// bias gradient sum_p zbar_v to g_bias.
+// dW += zbar h_prev^T over the workgroup tile, in two passes of two jet components: (v, L)
+// first, then (J0, J1). h_prev = tanh_jet(zp) is rebuilt from the previous layer's
+// pre-activation (or, with kFromLayer0, from layer 0's closed form
+// z = (c (W0 x + b0), W0[:,0], W0[:,1], 0)); one tanh per value serves both passes, and its
+// (v', s) are returned in (pv, ps) for the previous layer's own adjoint. Adds the bias
+// gradient sum_p zbar_v / c to g_bias.
 template <bool kFromLayer0>
 __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&zp)[4][4],
                                              f4 (&dw)[4], float& g_bias, float* stage_lane,
-                                             const float* stage_cols, const float* s_small,
-                                             int w, int g, float x0, float x1) {
+                                             const float* stage_rows, const float* s_small,
+                                             int w, int g, float x0, float x1, f4 (&pv)[4],
+                                             f4 (&ps)[4]) {
+  __syncthreads();  // previous readers of the staging buffer are done
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    __syncthreads();  // previous readers of the staging buffer are done
+  for (int mb = 0; mb < 4; ++mb) {
+    Layer0Weights w0;
+    if (kFromLayer0) w0 = layer0_weights(s_small, mb, g);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      Layer0Weights w0;
-      if (kFromLayer0) w0 = layer0_weights(s_small, mb, g);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float pv, pj0, pj1, pl;
-        if (kFromLayer0) {
-          pv = __builtin_fmaf(w0.wx[r], x0, __builtin_fmaf(w0.wy[r], x1, w0.b[r]));
-          pj0 = w0.wx[r];
-          pj1 = w0.wy[r];
-          pl = 0.0f;
-        } else {
-          pv = zp[mb][0][r];
-          pj0 = zp[mb][1][r];
-          pj1 = zp[mb][2][r];
-          pl = zp[mb][3][r];
-        }
-        float hv, hj0, hj1, hl;
-        tanh_jet(pv, pj0, pj1, pl, hv, hj0, hj1, hl);
-        if (half == 0) {
-          stage_write(stage_lane, mb, r, zbar[mb][0][r], zbar[mb][1][r], hv, hj0);
-        } else {
-          stage_write(stage_lane, mb, r, zbar[mb][2][r], zbar[mb][3][r], hj1, hl);
-        }
+    for (int r = 0; r < 4; ++r) {
+      float v, sl, l;
+      if (kFromLayer0) {
+        tanh_scaled(layer0_zv(w0, r, x0, x1), v, sl);
+        l = sl * (v * w0.q[r]);
+      } else {
+        tanh_scaled(zp[mb][0][r], v, sl);
+        const float q = __builtin_fmaf(zp[mb][1][r], zp[mb][1][r], zp[mb][2][r] * zp[mb][2][r]);
+        l = sl * __builtin_fmaf(v, q, zp[mb][3][r]);
       }
+      pv[mb][r] = v;
+      ps[mb][r] = sl;
+      stage_write(stage_lane, mb, r, zbar[mb][0][r], zbar[mb][3][r], v, l);
     }
-    __syncthreads();
-    const float bias = dw_product(stage_cols, w, dw);
-    if (half == 0) g_bias += sum_lane_groups(bias);
   }
+  __syncthreads();
+  g_bias += sum_lane_groups(dw_product(stage_rows, w, dw));
+  __syncthreads();
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    Layer0Weights w0;
+    if (kFromLayer0) w0 = layer0_weights(s_small, mb, g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float zj0 = kFromLayer0 ? w0.wx[r] : zp[mb][1][r];
+      const float zj1 = kFromLayer0 ? w0.wy[r] : zp[mb][2][r];
+      stage_write(stage_lane, mb, r, zbar[mb][1][r], zbar[mb][2][r], ps[mb][r] * zj0,
+                  ps[mb][r] * zj1);
+    }
+  }
+  __syncthreads();
+  dw_product(stage_rows, w, dw);
 }
 
 // Only z of hidden layers 2 and 3 is kept from the forward recompute; z of hidden layer 1 is
@@ -457,7 +628,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ __attribute__((aligned(16))) float s_stage[4 * kPlane];
   __shared__ float s_red[kBwdWaves];
-  stage_parameters(params, s_w, s_small, threadIdx.x, kBwdWaves * kWave);
+  stage_parameters<kBwdWaves * kWave>(params, s_w, s_small, threadIdx.x);
   __syncthreads();
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -466,8 +637,8 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   const int g = lane >> 4;
   const float* w_rows = s_w + lane_rows(m, g);
   const float* w_cols = s_w + lane_cols(m, g);
-  float* stage_lane = s_stage + 1088 * w + lane_rows(m, g);
-  const float* stage_cols = s_stage + lane_cols(m, g);
+  float* stage_lane = s_stage + lane_cols(m, g) + 16 * w;
+  const float* stage_rows = s_stage + lane_rows(m, g);
 
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
     f4 dw[3][4];
@@ -480,6 +651,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     float g_w0x = 0.f, g_w0y = 0.f, g_b0 = 0.f, g_wout = 0.f, g_bout = 0.f;
 
     for (int64_t tile = slot; tile < tiles; tile += slots) {
+      keep_lds_reads_in_loop();
       const int64_t point = tile * kBwdTile + kTile * w + m;
       const bool active = point < batch;
       float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f;
@@ -496,30 +668,34 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       layer0_forward(s_small, g, x0, x1, h);
       {
         f4 z1[4][4];
-        bias_init(s_small, 0, g, z1);
-        hidden_product(w_rows, h, z1);
+        hidden_layer(s_small, w_rows, 0, g, h, z1);
         apply_tanh_jet(z1, h);
       }
-      bias_init(s_small, 1, g, z2);
-      hidden_product(w_rows + kPlane, h, z2);
+      hidden_layer(s_small, w_rows, 1, g, h, z2);
       apply_tanh_jet(z2, h);
-      bias_init(s_small, 2, g, z3);
-      hidden_product(w_rows + 2 * kPlane, h, z3);
-      apply_tanh_jet(z3, h);
+      hidden_layer(s_small, w_rows, 2, g, h, z3);
+      f4 tv[4], ts[4];  // (v', s) of the layer whose adjoint comes next
+      apply_tanh_jet_vs(z3, h, tv, ts);
 
       // ---- 2. output layer: w_out / b_out gradients and the adjoint seed ----
       __syncthreads();  // the staging buffer is free
+      // In the scaled jet u = (w_out / c) . v' and lap = (w_out / lambda) . L', so
+      // dw_out = sum_p (gu / c) v' + (gl / lambda) L' and the seeds are vbar' = gu w_out / c,
+      // Lbar' = gl w_out / lambda, Jbar = 0.
       f4 hb[4][4];
+      const float gu_c = gu * (1.0f / kC);
+      const float gl_l = gl * (1.0f / kLambda);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        const f4 wo = lds4(s_small + kSmallWout + 16 * mb + 4 * g);
+        const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+        const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          stage_lane[16 * mb + r] = __builtin_fmaf(gu, h[mb][0][r], gl * h[mb][3][r]);
-          hb[mb][0][r] = gu * wo[r];
+          stage_lane[1088 * mb + kWRow * r] = __builtin_fmaf(gu_c, h[mb][0][r], gl_l * h[mb][3][r]);
+          hb[mb][0][r] = gu * wv[r];
           hb[mb][1][r] = 0.0f;
           hb[mb][2][r] = 0.0f;
-          hb[mb][3][r] = gl * wo[r];
+          hb[mb][3][r] = gl * wl[r];
         }
       }
       {
@@ -531,45 +707,49 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         if (lane == 0) s_red[w] = su;
       }
       __syncthreads();
-      g_wout += plane_sum(stage_cols, 0, w);
+      g_wout += plane_sum(stage_rows, 0, w);
       g_bout += ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
 
       // ---- 3. hidden layer 3 ----
-      tanh_adjoint_in_place(z3, hb);
-      stage_and_dw<false>(z3, z2, dw[2], g_bh[2], stage_lane, stage_cols, s_small, w, g, x0, x1);
+      tanh_adjoint_in_place(z3, hb, tv, ts);
+      stage_and_dw<false>(z3, z2, dw[2], g_bh[2], stage_lane, stage_rows, s_small, w, g, x0, x1,
+                          tv, ts);
       hidden_product_t(w_cols + 2 * kPlane, z3, hb);
 
       // ---- 4. hidden layer 2 (needs hidden layer 1's z: recompute it) ----
-      tanh_adjoint_in_place(z2, hb);
+      tanh_adjoint_in_place(z2, hb, tv, ts);
       f4 z1[4][4];
       layer0_forward(s_small, g, x0, x1, h);
-      bias_init(s_small, 0, g, z1);
-      hidden_product(w_rows, h, z1);
-      stage_and_dw<false>(z2, z1, dw[1], g_bh[1], stage_lane, stage_cols, s_small, w, g, x0, x1);
+      hidden_layer(s_small, w_rows, 0, g, h, z1);
+      stage_and_dw<false>(z2, z1, dw[1], g_bh[1], stage_lane, stage_rows, s_small, w, g, x0, x1,
+                          tv, ts);
       hidden_product_t(w_cols + kPlane, z2, hb);
 
       // ---- 5. hidden layer 1 ----
-      tanh_adjoint_in_place(z1, hb);
-      stage_and_dw<true>(z1, z1, dw[0], g_bh[0], stage_lane, stage_cols, s_small, w, g, x0, x1);
+      tanh_adjoint_in_place(z1, hb, tv, ts);
+      stage_and_dw<true>(z1, z1, dw[0], g_bh[0], stage_lane, stage_rows, s_small, w, g, x0, x1,
+                         tv, ts);
       hidden_product_t(w_cols, z1, hb);
 
       // ---- 6. layer 0 in closed form ----
+      // bv is the adjoint of c z_v, so zbar_v = c bv: grad_x = (c W0)^T bv,
+      // dW0[o][d] = sum_p bv (c x_d) + zbar_Jd, db0 = c sum_p bv.
       float gx0 = 0.f, gx1 = 0.f;
+      const float cx0 = kC * x0, cx1 = kC * x1;
       __syncthreads();  // staging buffer free again
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const Layer0Weights w0 = layer0_weights(s_small, mb, g);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float zv = __builtin_fmaf(w0.wx[r], x0, __builtin_fmaf(w0.wy[r], x1, w0.b[r]));
           float bv = hb[mb][0][r], bj0 = hb[mb][1][r], bj1 = hb[mb][2][r], bl = hb[mb][3][r];
-          tanh_jet_adjoint(zv, w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
-          gx0 = __builtin_fmaf(w0.wx[r], bv, gx0);
-          gx1 = __builtin_fmaf(w0.wy[r], bv, gx1);
-          float* p = stage_lane + 16 * mb + r;
-          p[0] = __builtin_fmaf(bv, x0, bj0);       // dW0[o][0] contribution
-          p[kPlane] = __builtin_fmaf(bv, x1, bj1);  // dW0[o][1]
-          p[2 * kPlane] = bv;                       // db0[o]
+          tanh_jet_adjoint_vs(tv[mb][r], ts[mb][r], w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
+          gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
+          gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
+          float* p = stage_lane + 1088 * mb + kWRow * r;
+          p[0] = __builtin_fmaf(bv, cx0, bj0);       // dW0[o][0] contribution
+          p[kPlane] = __builtin_fmaf(bv, cx1, bj1);  // dW0[o][1]
+          p[2 * kPlane] = bv;                        // db0[o] / c
         }
       }
       gx0 = sum_lane_groups(gx0);
@@ -579,9 +759,9 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         grad_coordinates[2 * point + 1] = gx1;
       }
       __syncthreads();
-      g_w0x += plane_sum(stage_cols, 0, w);
-      g_w0y += plane_sum(stage_cols, 1, w);
-      g_b0 += plane_sum(stage_cols, 2, w);
+      g_w0x += plane_sum(stage_rows, 0, w);
+      g_w0y += plane_sum(stage_rows, 1, w);
+      g_b0 += plane_sum(stage_rows, 2, w);
     }
 
     // ---- this slot's partial row: every entry written by exactly one lane ----
@@ -594,13 +774,13 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 #pragma unroll
         for (int r = 0; r < 4; ++r) wrow[(16 * w + 4 * g + r) * kHidden + 16 * nb + m] = dw[l][nb][r];
       }
-      if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = g_bh[l];
+      if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * g_bh[l];  // bias sums are of c^-1 zbar_v
     }
     if (g == 0) {
       const int o = 16 * w + m;
       row[kInputs * o] = g_w0x;
       row[kInputs * o + 1] = g_w0y;
-      row[kLayer0Bias + o] = g_b0;
+      row[kLayer0Bias + o] = kC * g_b0;
       row[kOutputBase + o] = g_wout;
     }
     if (threadIdx.x == 0) row[kOutputBase + kHidden] = g_bout;
@@ -731,9 +911,16 @@ extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* pa
   if (int st = current_device_cus(&cus)) return st;
   const int64_t tiles = (batch + kTile - 1) / kTile;
   const int grid = static_cast<int>(std::min<int64_t>(tiles, cus));
-  hipLaunchKernelGGL(forward_kernel<kFwdWaves>, dim3(grid), dim3(kFwdWaves * kWave), 0,
-                     static_cast<hipStream_t>(stream), coordinates, parameters, output, laplacian,
-                     batch, tiles);
+  // FUSED_HOAD_FWD_WAVES (experiment knob, read per call) picks 8 or 12 waves per workgroup.
+  const char* env = std::getenv("FUSED_HOAD_FWD_WAVES");
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (env && std::atoi(env) == 12) {
+    hipLaunchKernelGGL(forward_kernel<12>, dim3(grid), dim3(12 * kWave), 0, hs, coordinates,
+                       parameters, output, laplacian, batch, tiles);
+  } else {
+    hipLaunchKernelGGL(forward_kernel<kFwdWaves>, dim3(grid), dim3(kFwdWaves * kWave), 0, hs,
+                       coordinates, parameters, output, laplacian, batch, tiles);
+  }
   return check_launch("forward_kernel");
 }
 
