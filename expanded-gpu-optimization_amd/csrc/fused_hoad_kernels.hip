@@ -399,9 +399,39 @@ __device__ __forceinline__ void layer0_forward(const float* s_small, int g, floa
 // them as per-tile LDS reads.
 __device__ __forceinline__ void keep_lds_reads_in_loop() { __asm__ volatile("" ::: "memory"); }
 
+// Value of lane l ^ 32 (permlane32) or l ^ 16 (permlane16) in every lane, with gfx950's
+// v_permlane32_swap / v_permlane16_swap (VALU, no LDS round trip). swap(u, 0) leaves the
+// partner in .second of the low half, swap(0, u) in .first of the high half, and the other
+// halves are zero. (Swapping a register with a copy of itself would need one swap, but the
+// compiler folds that form to the wrong result.)
+__device__ __forceinline__ float partner32(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, 0u, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(0u, u, false, false);
+  return __builtin_bit_cast(float, a[1] | b[0]);
+}
+
+__device__ __forceinline__ float partner16(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, 0u, false, false);
+  const auto b = __builtin_amdgcn_permlane16_swap(0u, u, false, false);
+  return __builtin_bit_cast(float, a[1] | b[0]);
+}
+
+// x[l] + x[l ^ 32] + x[l ^ 16] + x[l ^ 48] in every lane, bitwise identical across the four
+// lanes (each pairwise sum adds the same two operands).
 __device__ __forceinline__ float sum_lane_groups(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
+  const float y = x + partner32(x);
+  return y + partner16(y);
+}
+
+// Sum over the 16 lanes of a row (lanes 16 g .. 16 g + 15), identical in all 16 lanes: DPP
+// butterflies xor 1 and xor 2 (quad_perm), then the 8- and 16-lane mirrors.
+__device__ __forceinline__ float sum_row16(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true));
   return x;
 }
 
@@ -475,7 +505,7 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
 // One workgroup per CU, 4 waves (one per SIMD, up to 512 registers each), 64-point workgroup
 // tiles (16 points per wave). Per tile:
 //   1. every wave re-runs the forward for its 16 points, keeping the pre-activations z in
-//      registers;
+//      registers (hidden layer 1's in a per-wave stash, see below);
 //   2. the adjoint is seeded from the linear output layer and walked back through layers 3..1:
 //      tanh-jet adjoint in registers, dW += zbar h_prev^T, hbar = W^T zbar (registers), and
 //      finally layer 0 in closed form;
@@ -490,6 +520,7 @@ constexpr int kBwdWaves = 4;
 constexpr int kBwdTile = kBwdWaves * kTile;  // 64 points
 constexpr int kMaxSlots = 256;
 constexpr int kRowStride = 12800;            // floats per partial row (>= 12737)
+constexpr int kStashF4PerWave = 16 * kWave;  // hidden layer 1's z for one wave tile (16 KB)
 constexpr int kReduceGroups = 16;            // fixed reduction tree: 16 groups of 16 slots
 static_assert(kMaxSlots % kReduceGroups == 0, "reduction tree must tile the slots");
 
@@ -616,14 +647,15 @@ __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&
   dw_product(stage_rows, w, dw);
 }
 
-// Only z of hidden layers 2 and 3 is kept from the forward recompute; z of hidden layer 1 is
-// recomputed from x just before it is needed. That keeps the live state near 240 registers
-// per lane, so nothing spills.
+// z of hidden layers 2 and 3 stays in registers through the walk back; z of hidden layer 1
+// would push the live state past the register file, so each wave parks it in its own 16 KB
+// of the workspace (`stash`, coalesced 16-byte stores, L2-resident) and reloads it after
+// layer 3, into the registers layer 3's zbar leaves free.
 __global__ void __launch_bounds__(kBwdWaves * kWave, 1)
 backward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                 const float* __restrict__ grad_output, const float* __restrict__ grad_laplacian,
                 float* __restrict__ grad_coordinates, float* __restrict__ partials,
-                int64_t batch, int64_t tiles, int slots) {
+                f4* __restrict__ stash, int64_t batch, int64_t tiles, int slots) {
   __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ __attribute__((aligned(16))) float s_stage[4 * kPlane];
@@ -638,6 +670,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   const float* w_rows = s_w + lane_rows(m, g);
   const float* w_cols = s_w + lane_cols(m, g);
   float* stage_lane = s_stage + lane_cols(m, g) + 16 * w;
+  f4* my_stash = stash + static_cast<int64_t>(blockIdx.x * kBwdWaves + w) * kStashF4PerWave + lane;
   const float* stage_rows = s_stage + lane_rows(m, g);
 
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
@@ -669,6 +702,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       {
         f4 z1[4][4];
         hidden_layer(s_small, w_rows, 0, g, h, z1);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) my_stash[(4 * mb + c) * kWave] = z1[mb][c];
+        }
+        keep_lds_reads_in_loop();  // issue the stores here, so z1 is not held until later
         apply_tanh_jet(z1, h);
       }
       hidden_layer(s_small, w_rows, 1, g, h, z2);
@@ -699,11 +738,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         }
       }
       {
-        float su = gu;
-        su += __shfl_xor(su, 1);
-        su += __shfl_xor(su, 2);
-        su += __shfl_xor(su, 4);
-        su += __shfl_xor(su, 8);
+        const float su = sum_row16(gu);
         if (lane == 0) s_red[w] = su;
       }
       __syncthreads();
@@ -716,11 +751,15 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
                           tv, ts);
       hidden_product_t(w_cols + 2 * kPlane, z3, hb);
 
-      // ---- 4. hidden layer 2 (needs hidden layer 1's z: recompute it) ----
-      tanh_adjoint_in_place(z2, hb, tv, ts);
+      // ---- 4. hidden layer 2 (needs hidden layer 1's z back from the stash) ----
+      keep_lds_reads_in_loop();  // the reload below must read memory, not forward the stores
       f4 z1[4][4];
-      layer0_forward(s_small, g, x0, x1, h);
-      hidden_layer(s_small, w_rows, 0, g, h, z1);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) z1[mb][c] = my_stash[(4 * mb + c) * kWave];
+      }
+      tanh_adjoint_in_place(z2, hb, tv, ts);
       stage_and_dw<false>(z2, z1, dw[1], g_bh[1], stage_lane, stage_rows, s_small, w, g, x0, x1,
                           tv, ts);
       hidden_product_t(w_cols + kPlane, z2, hb);
@@ -924,9 +963,12 @@ extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* pa
   return check_launch("forward_kernel");
 }
 
+// Workspace: `slots` partial rows, then one z stash per (workgroup, wave); the grid never
+// exceeds `slots`, so both are sized by it.
 extern "C" size_t fhoad_backward_workspace_size(int64_t batch) {
   if (batch <= 0) return 0;
-  return static_cast<size_t>(backward_slots(batch)) * kRowStride * sizeof(float);
+  const size_t slots = static_cast<size_t>(backward_slots(batch));
+  return slots * (kRowStride * sizeof(float) + kBwdWaves * kStashF4PerWave * sizeof(f4));
 }
 
 extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const float* parameters,
@@ -967,9 +1009,10 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
     if (cap > 0) grid = static_cast<int>(std::min<long>(grid, cap));
   }
   float* partials = static_cast<float*>(workspace);
+  f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
   hipLaunchKernelGGL(backward_kernel, dim3(grid), dim3(kBwdWaves * kWave), 0, hs, coordinates,
-                     parameters, grad_output, grad_laplacian, grad_coordinates, partials, batch,
-                     tiles, slots);
+                     parameters, grad_output, grad_laplacian, grad_coordinates, partials, stash,
+                     batch, tiles, slots);
   if (int st = check_launch("backward_kernel")) return st;
   hipLaunchKernelGGL(reduce_partials_kernel, dim3((kParameterCount + 63) / 64),
                      dim3(kReduceGroups * 64), 0, hs, partials, slots, grad_parameters);

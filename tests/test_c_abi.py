@@ -68,15 +68,15 @@ def test_constants_and_status_strings() -> None:
     assert lib.fhoad_status_string(4) == b"workspace too small"
 
 
-def test_workspace_size_is_one_partial_row_per_slot() -> None:
+def test_workspace_size_is_one_partial_row_and_stash_per_slot() -> None:
     lib = _lib()
     assert lib.fhoad_backward_workspace_size(0) == 0
-    row = 12800 * 4
-    assert lib.fhoad_backward_workspace_size(1) == row
-    assert lib.fhoad_backward_workspace_size(64) == row
-    assert lib.fhoad_backward_workspace_size(65) == 2 * row
-    assert lib.fhoad_backward_workspace_size(65536) == 256 * row
-    assert lib.fhoad_backward_workspace_size(1 << 20) == 256 * row
+    per_slot = 12800 * 4 + 4 * 16 * 1024  # partial row + four 16 KB per-wave stashes
+    assert lib.fhoad_backward_workspace_size(1) == per_slot
+    assert lib.fhoad_backward_workspace_size(64) == per_slot
+    assert lib.fhoad_backward_workspace_size(65) == 2 * per_slot
+    assert lib.fhoad_backward_workspace_size(65536) == 256 * per_slot
+    assert lib.fhoad_backward_workspace_size(1 << 20) == 256 * per_slot
 
 
 def test_argument_errors_are_reported_before_any_device_work() -> None:
