@@ -2,9 +2,13 @@
 
 Metric: residual points/s (u, Laplacian u) at 64K points plus train-step ms at
 64K points, FP32, 1 GPU. One "step" is one fused residual evaluation of 65,536 points
-(coordinates already in HBM); the training step (fused forward + loss + fused backward + Adam
-lr 1e-3 on mean((Laplacian u - f)^2), f = -2 pi^2 sin(pi x) sin(pi y)) is timed the same way at
-65,536 points and reported as ``train_step_ms``.
+(coordinates already in HBM). The training step (forward jet, loss mean((Laplacian u - f)^2)
+with f = -2 pi^2 sin(pi x) sin(pi y), adjoint jet, Adam lr 1e-3) is timed the same way at 65,536
+points: ``train_step_ms`` is the fused step (FusedPoissonAdam: one gradient kernel that re-runs
+the forward and seeds itself from the loss, one reduction kernel with the Adam update),
+``train_step_graphed_ms`` the same replayed from a HIP graph, and ``train_step_autograd_ms``
+the reference's step through the drop-in API (fused forward + autograd loss + fused backward +
+torch.optim.Adam).
 
 Correctness is checked before any timing: the fused forward against the package's PyTorch
 forward Laplacian (atol 1e-5 / rtol 1e-4) and the fused backward against the PyTorch
@@ -108,6 +112,7 @@ def main() -> None:
     )
     from fused_hoad.backends.fused import _recompute_backward, fused_laplacian
     from fused_hoad.parameters import pack_poisson_parameters
+    from fused_hoad.training import FusedPoissonAdam
 
     load_extension()  # fail loudly if the HIP extension is missing
     if not torch.cuda.is_available():
@@ -168,27 +173,63 @@ def main() -> None:
         log(f"backward call {args.train_points} pts: {bwd_ms * 1e3:.1f} us (events, mean)")
         return
 
-    # ---- training step: fused forward + loss + fused backward + Adam ----
+    # ---- training step (a): the reference's step through the drop-in API ----
+    # fused forward (autograd.Function) + mean((Lap u - f)^2) + fused backward + torch Adam
+    # (/root/reference/benchmarks/benchmark_training.py:41-60).
     optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)
     source = manufactured_source(x_train)
 
-    def train_step():
+    def autograd_step():
         optimizer.zero_grad(set_to_none=True)
         _, lap_t = fused_laplacian(model, x_train)
         (lap_t - source).pow(2).mean().backward()
         optimizer.step()
 
     for _ in range(args.warmup):
-        train_step()
+        autograd_step()
+    autograd_total_ms, autograd_calls = _events_timed(autograd_step, args.steps, torch)
+    autograd_ms = autograd_total_ms / args.steps
+    log(f"train step (autograd drop-in) {args.train_points} pts: {autograd_ms:.3f} ms wall/step, "
+        f"median {statistics.median(autograd_calls):.3f} ms (events)")
+
+    # ---- training step (b): the fused step, FusedPoissonAdam (2 kernels) ----
+    torch.manual_seed(0)
+    fused_model = build_mlp(DEFAULT_POISSON_MLP).to(device)
+    trainer = FusedPoissonAdam(fused_model, x_train, source, lr=1e-3)
+    # check the first step before timing: loss against the fused forward's, gradient against
+    # the recompute backward seeded with grad_lap = 2 (lap - f) / B
+    with torch.no_grad():
+        _, lap0 = fused_forward_laplacian(x_train, trainer.parameters)
+    resid0 = lap0 - source
+    want_loss = resid0.double().pow(2).mean().item()
+    _, want_grad = _recompute_backward(x_train, trainer.parameters.clone(), torch.zeros_like(lap0),
+                                       2.0 * resid0 / args.train_points, False, True)
+    got_loss = trainer.step().item()
+    step_err = _scaled_error(trainer.grad, want_grad)
+    if abs(got_loss - want_loss) > 1e-5 * abs(want_loss) or step_err > 1e-4:
+        raise SystemExit(f"fused step disagrees: loss {got_loss} vs {want_loss}, gradient {step_err:.3e}")
+    log(f"check: fused step loss rel error {abs(got_loss - want_loss) / want_loss:.2e}, "
+        f"gradient max scaled error {step_err:.2e}")
+    for _ in range(args.warmup):
+        trainer.step()
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats(device)
     baseline_bytes = torch.cuda.memory_allocated(device)
-    train_total_ms, train_calls = _events_timed(train_step, args.steps, torch)
+    train_total_ms, train_calls = _events_timed(trainer.step, args.steps, torch)
     train_ms = train_total_ms / args.steps
     peak_mib = (torch.cuda.max_memory_allocated(device) - baseline_bytes) / 2**20
-    log(f"train step {args.train_points} pts: {train_ms:.3f} ms wall/step, "
+    log(f"train step (fused) {args.train_points} pts: {train_ms:.3f} ms wall/step, "
         f"median {statistics.median(train_calls):.3f} ms (events); backward call {bwd_ms * 1e3:.1f} us; "
         f"peak {peak_mib:.1f} MiB above baseline")
+
+    # ---- training step (c): the fused step replayed from a HIP graph ----
+    replay = trainer.graphed(warmup=1)
+    for _ in range(args.warmup):
+        replay()
+    graph_total_ms, graph_calls = _events_timed(replay, args.steps, torch)
+    graph_ms = graph_total_ms / args.steps
+    log(f"train step (fused, HIP graph) {args.train_points} pts: {graph_ms:.3f} ms wall/step, "
+        f"median {statistics.median(graph_calls):.3f} ms (events)")
 
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * 2**20 // 4
@@ -228,6 +269,15 @@ def main() -> None:
     }
     step_flop = (FLOP_PER_POINT_FORWARD + FLOP_PER_POINT_BACKWARD) * args.train_points
     train_tflops = step_flop / (train_ms / 1e3) / 1e12
+    roofline_train_step = {
+        "bound": "mfma",
+        "achieved": round(train_tflops, 3),
+        "peak": PEAK_FP32_MATRIX_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(train_tflops / PEAK_FP32_MATRIX_TFLOPS, 4),
+        "kernel": "fused step: backward_kernel<loss> + reduce_adam_kernel, wall time per step",
+        "flop_per_step": step_flop,
+    }
 
     cpu_baseline = None
     if not args.no_cpu_baseline:
@@ -248,17 +298,22 @@ def main() -> None:
         "data": "synthetic (coordinates U[-1,1]^2 from a seeded CPU generator; torch.manual_seed(0) default nn.Linear init)",
         "config": {
             "workload": "fused residual (u, Laplacian u) of the 2->64x4->1 tanh MLP at 65,536 points; "
-                        "train step = fused forward + mean((Lap u - f)^2) + fused backward + Adam(lr 1e-3) at 65,536 points",
+                        "train step = forward jet + mean((Lap u - f)^2) + adjoint jet + Adam(lr 1e-3) at 65,536 points "
+                        "(train_step_ms: the fused step, FusedPoissonAdam; train_step_autograd_ms: the same step "
+                        "through fused_laplacian + autograd + torch.optim.Adam)",
             "points": args.points,
             "train_points": args.train_points,
         },
         "train_step_ms": round(train_ms, 5),
         "train_step_tflops": round(train_tflops, 3),
         "train_step_peak_mib": round(peak_mib, 2),
+        "train_step_graphed_ms": round(graph_ms, 5),
+        "train_step_autograd_ms": round(autograd_ms, 5),
         "backward_call_ms": round(bwd_ms, 5),
         "gpu_clock_mhz": clock,
         "roofline": roofline,
         "roofline_backward": roofline_backward,
+        "roofline_train_step": roofline_train_step,
         "cpu_baseline": cpu_baseline,
         "reference_published": REFERENCE_A5000,
     }

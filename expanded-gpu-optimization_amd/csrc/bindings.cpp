@@ -97,7 +97,62 @@ std::vector<torch::Tensor> fused_forward_laplacian_backward(torch::Tensor coordi
   return {grad_parameters, grad_coordinates};
 }
 
+// One fused Poisson + Adam training step (fhoad_poisson_adam_step). No counterpart among the
+// reference's bindings: it replaces the Python step of
+// /root/reference/benchmarks/benchmark_training.py:41-60 (fused forward, loss, fused backward,
+// torch.optim.Adam). parameters, exp_avg, exp_avg_sq and step are updated in place; returns the
+// loss (a 0-dim tensor) of the parameters on entry.
+torch::Tensor poisson_adam_step(torch::Tensor coordinates, torch::Tensor source,
+                                torch::Tensor parameters, torch::Tensor exp_avg,
+                                torch::Tensor exp_avg_sq, torch::Tensor step, double lr,
+                                double beta1, double beta2, double eps, double weight_decay,
+                                c10::optional<torch::Tensor> grad_parameters,
+                                c10::optional<torch::Tensor> grad_coordinates) {
+  check_inputs(coordinates, parameters);
+  const int64_t batch = coordinates.size(0);
+  TORCH_CHECK(batch > 0, "coordinates must hold at least one point");
+  auto check_like = [&](const torch::Tensor& t, int64_t numel, const char* what) {
+    TORCH_CHECK(t.is_cuda() && t.is_contiguous() && t.scalar_type() == torch::kFloat32, what,
+                " must be a contiguous float32 CUDA tensor");
+    TORCH_CHECK(t.numel() == numel, what, " must have ", numel, " values");
+    TORCH_CHECK(t.device() == coordinates.device(), what, " must be on the coordinates' device");
+  };
+  check_like(source, batch, "source");
+  check_like(exp_avg, kParameterCount, "exp_avg");
+  check_like(exp_avg_sq, kParameterCount, "exp_avg_sq");
+  check_like(step, 1, "step");
+  float* grad_parameters_ptr = nullptr;
+  float* grad_coordinates_ptr = nullptr;
+  if (grad_parameters.has_value()) {
+    check_like(*grad_parameters, kParameterCount, "grad_parameters");
+    grad_parameters_ptr = grad_parameters->data_ptr<float>();
+  }
+  if (grad_coordinates.has_value()) {
+    check_like(*grad_coordinates, 2 * batch, "grad_coordinates");
+    grad_coordinates_ptr = grad_coordinates->data_ptr<float>();
+  }
+  const c10::DeviceGuard device_guard(coordinates.device());
+  auto loss = torch::empty({}, coordinates.options());
+  const size_t workspace_bytes = fhoad_backward_workspace_size(batch);
+  auto workspace = torch::empty({static_cast<int64_t>(workspace_bytes)},
+                                coordinates.options().dtype(torch::kUInt8));
+  check_status(fhoad_poisson_adam_step(
+      coordinates.data_ptr<float>(), source.data_ptr<float>(), parameters.data_ptr<float>(),
+      exp_avg.data_ptr<float>(), exp_avg_sq.data_ptr<float>(), step.data_ptr<float>(),
+      loss.data_ptr<float>(), grad_parameters_ptr, grad_coordinates_ptr, workspace.data_ptr(),
+      workspace_bytes, batch, lr, beta1, beta2, eps, weight_decay, current_stream(coordinates)));
+  return loss;
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
+  module.def("poisson_adam_step", &poisson_adam_step,
+             "Fused Poisson-loss training step with Adam on the packed parameters (MI355X)",
+             pybind11::arg("coordinates"), pybind11::arg("source"), pybind11::arg("parameters"),
+             pybind11::arg("exp_avg"), pybind11::arg("exp_avg_sq"), pybind11::arg("step"),
+             pybind11::arg("lr"), pybind11::arg("beta1"), pybind11::arg("beta2"),
+             pybind11::arg("eps"), pybind11::arg("weight_decay"),
+             pybind11::arg("grad_parameters") = pybind11::none(),
+             pybind11::arg("grad_coordinates") = pybind11::none());
   module.def("fused_forward_laplacian", &fused_forward_laplacian,
              "Fixed MLP forward pass and input Laplacian (MI355X HIP kernel)",
              pybind11::arg("coordinates"), pybind11::arg("parameters"),

@@ -647,19 +647,40 @@ __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&
   dw_product(stage_rows, w, dw);
 }
 
+// Seed of the fused Poisson training step (kLoss): the loss is mean((lap - f)^2) over the
+// batch, so the backward needs grad_u = 0 and grad_lap = (1 / B) (2 r) with r = lap - f,
+// exactly the upstream gradients autograd forms for (lap - f).pow(2).mean()
+// (/root/reference/benchmarks/benchmark_training.py:46-48). The kernel already re-runs the
+// forward, so it forms lap, r and the seed itself; sum r^2 goes into column kLossColumn of the
+// slot's partial row. `step` is the Adam step counter, advanced here (one lane of workgroup 0)
+// so that the update kernel that follows reads a settled value.
+struct LossSeed {
+  const float* source;  // f[batch]
+  float inv_batch;      // fl(1 / B)
+  float* step;          // Adam step counter (one float)
+};
+
+constexpr int kLossColumn = kParameterCount;  // partial-row column of sum r^2
+static_assert(kLossColumn < kRowStride, "the loss column must fit in a partial row");
+
 // z of hidden layers 2 and 3 stays in registers through the walk back; z of hidden layer 1
 // would push the live state past the register file, so each wave parks it in its own 16 KB
 // of the workspace (`stash`, coalesced 16-byte stores, L2-resident) and reloads it after
 // layer 3, into the registers layer 3's zbar leaves free.
+//
+// kLoss: grad_output and grad_laplacian are unused and the seed comes from `seed` (above);
+// grad_coordinates may be null.
+template <bool kLoss>
 __global__ void __launch_bounds__(kBwdWaves * kWave, 1)
 backward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                 const float* __restrict__ grad_output, const float* __restrict__ grad_laplacian,
                 float* __restrict__ grad_coordinates, float* __restrict__ partials,
-                f4* __restrict__ stash, int64_t batch, int64_t tiles, int slots) {
+                f4* __restrict__ stash, int64_t batch, int64_t tiles, int slots, LossSeed seed) {
   __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ __attribute__((aligned(16))) float s_stage[4 * kPlane];
   __shared__ float s_red[kBwdWaves];
+  if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] += 1.0f;
   stage_parameters<kBwdWaves * kWave>(params, s_w, s_small, threadIdx.x);
   __syncthreads();
 
@@ -682,17 +703,22 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     }
     float g_bh[3] = {0.f, 0.f, 0.f};
     float g_w0x = 0.f, g_w0y = 0.f, g_b0 = 0.f, g_wout = 0.f, g_bout = 0.f;
+    float g_loss = 0.f;  // kLoss: this wave's sum of r^2 over the slot's tiles
 
     for (int64_t tile = slot; tile < tiles; tile += slots) {
       keep_lds_reads_in_loop();
       const int64_t point = tile * kBwdTile + kTile * w + m;
       const bool active = point < batch;
-      float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f;
+      float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f, f = 0.f;
       if (active) {
         x0 = coordinates[2 * point];
         x1 = coordinates[2 * point + 1];
-        gu = grad_output[point];
-        gl = grad_laplacian[point];
+        if (kLoss) {
+          f = seed.source[point];
+        } else {
+          gu = grad_output[point];
+          gl = grad_laplacian[point];
+        }
       }
 
       // ---- 1. forward recompute ----
@@ -715,6 +741,21 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       hidden_layer(s_small, w_rows, 2, g, h, z3);
       f4 tv[4], ts[4];  // (v', s) of the layer whose adjoint comes next
       apply_tanh_jet_vs(z3, h, tv, ts);
+
+      if (kLoss) {
+        // lap = w_out . L in the forward kernel's order, then the residual seed.
+        float lap = 0.0f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) lap = __builtin_fmaf(wl[r], h[mb][3][r], lap);
+        }
+        lap = sum_lane_groups(lap);
+        const float res = active ? lap - f : 0.0f;
+        gl = seed.inv_batch * (2.0f * res);
+        g_loss += sum_row16(res * res);
+      }
 
       // ---- 2. output layer: w_out / b_out gradients and the adjoint seed ----
       __syncthreads();  // the staging buffer is free
@@ -793,7 +834,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       }
       gx0 = sum_lane_groups(gx0);
       gx1 = sum_lane_groups(gx1);
-      if (g == 0 && active) {
+      if (g == 0 && active && (!kLoss || grad_coordinates != nullptr)) {
         grad_coordinates[2 * point] = gx0;
         grad_coordinates[2 * point + 1] = gx1;
       }
@@ -823,6 +864,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       row[kOutputBase + o] = g_wout;
     }
     if (threadIdx.x == 0) row[kOutputBase + kHidden] = g_bout;
+    if (kLoss) {
+      __syncthreads();  // every wave is done with s_red
+      if (lane == 0) s_red[w] = g_loss;
+      __syncthreads();
+      if (threadIdx.x == 0) row[kLossColumn] = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
+    }
     __syncthreads();  // s_red and the staging buffer are reused by the next slot
   }
 }
@@ -830,15 +877,14 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 // grad[k] = sum over slots of partials[slot][k], in a fixed tree: 16 groups of 16 consecutive
 // slots are summed in slot order, then the 16 group sums in group order. Slots at or beyond
 // `slots` are skipped (they would add +0.0f).
-__global__ void __launch_bounds__(kReduceGroups * 64)
-reduce_partials_kernel(const float* __restrict__ partials, int slots, float* __restrict__ grad) {
-  __shared__ float s_part[kReduceGroups][64];
-  const int col = threadIdx.x & 63;
-  const int group = threadIdx.x >> 6;
-  const int k = blockIdx.x * 64 + col;
+// Column k's total over the slots, complete in the threads of group 0 (columns >= `columns`
+// read nothing and give 0).
+__device__ __forceinline__ float fixed_tree_sum(const float* __restrict__ partials, int slots,
+                                                int k, int columns, float (*s_part)[64],
+                                                int group, int col) {
   constexpr int kPerGroup = kMaxSlots / kReduceGroups;
   float acc = 0.0f;
-  if (k < kParameterCount) {
+  if (k < columns) {
     float v[kPerGroup];
 #pragma unroll
     for (int i = 0; i < kPerGroup; ++i) {
@@ -850,12 +896,80 @@ reduce_partials_kernel(const float* __restrict__ partials, int slots, float* __r
   }
   s_part[group][col] = acc;
   __syncthreads();
-  if (group == 0 && k < kParameterCount) {
-    float total = 0.0f;
+  float total = 0.0f;
+  if (group == 0) {
 #pragma unroll
     for (int i = 0; i < kReduceGroups; ++i) total += s_part[i][col];
-    grad[k] = total;
   }
+  return total;
+}
+
+__global__ void __launch_bounds__(kReduceGroups * 64)
+reduce_partials_kernel(const float* __restrict__ partials, int slots, float* __restrict__ grad) {
+  __shared__ float s_part[kReduceGroups][64];
+  const int col = threadIdx.x & 63;
+  const int group = threadIdx.x >> 6;
+  const int k = blockIdx.x * 64 + col;
+  const float total = fixed_tree_sum(partials, slots, k, kParameterCount, s_part, group, col);
+  if (group == 0 && k < kParameterCount) grad[k] = total;
+}
+
+// Adam (torch.optim.Adam, amsgrad = False, maximize = False) on the flat parameter buffer.
+struct AdamArgs {
+  float* params;
+  float* exp_avg;
+  float* exp_avg_sq;
+  const float* step;  // already advanced for this step by the gradient kernel
+  float* loss;        // mean r^2
+  float* grad;        // optional copy of the summed gradient (nullptr: none)
+  double lr, beta1, beta2, eps, weight_decay;
+  float inv_batch;
+};
+
+// The fixed-tree gradient sum of reduce_partials_kernel, then the Adam update of each
+// parameter in the same thread, so the summed gradient never goes through memory. Element
+// arithmetic follows torch's multi-tensor Adam (torch/optim/adam.py, _multi_tensor_adam):
+//   g += wd p;  m = lerp(m, g, 1 - b1);  v = v b2 + (1 - b2) g g;
+//   p += -(lr / bc1) m / (sqrt(v) / sqrt(bc2) + eps),  bc_i = 1 - b_i^t,
+// with the bias corrections in double and every tensor operation rounded to float. Column
+// kLossColumn gives loss = inv_batch * sum r^2.
+__global__ void __launch_bounds__(kReduceGroups * 64)
+reduce_adam_kernel(const float* __restrict__ partials, int slots, AdamArgs a) {
+  __shared__ float s_part[kReduceGroups][64];
+  const int col = threadIdx.x & 63;
+  const int group = threadIdx.x >> 6;
+  const int k = blockIdx.x * 64 + col;
+  const float total = fixed_tree_sum(partials, slots, k, kLossColumn + 1, s_part, group, col);
+  if (group != 0) return;
+  if (k == kLossColumn) {
+    a.loss[0] = total * a.inv_batch;
+    return;
+  }
+  if (k >= kParameterCount) return;
+  if (a.grad) a.grad[k] = total;
+  const double t = static_cast<double>(a.step[0]);
+  const double bc1 = 1.0 - pow(a.beta1, t);
+  const double bc2 = 1.0 - pow(a.beta2, t);
+  const float step_size = static_cast<float>(-(a.lr / bc1));
+  const float bc2_sqrt = static_cast<float>(sqrt(bc2));
+  const float w1 = static_cast<float>(1.0 - a.beta1);
+  const float b2 = static_cast<float>(a.beta2);
+  const float w2 = static_cast<float>(1.0 - a.beta2);
+  const float eps = static_cast<float>(a.eps);
+  const float wd = static_cast<float>(a.weight_decay);
+
+  float p = a.params[k];
+  float g = total;
+  if (wd != 0.0f) g = g + wd * p;
+  float m = a.exp_avg[k];
+  m = m + w1 * (g - m);  // lerp with weight < 0.5
+  float v = a.exp_avg_sq[k] * b2;
+  v = v + w2 * g * g;
+  const float denom = sqrtf(v) / bc2_sqrt + eps;
+  p = p + step_size * m / denom;
+  a.exp_avg[k] = m;
+  a.exp_avg_sq[k] = v;
+  a.params[k] = p;
 }
 
 __global__ void fill_zero_kernel(float* __restrict__ out, int64_t n) {
@@ -912,6 +1026,21 @@ int64_t backward_tiles(int64_t batch) { return (batch + kBwdTile - 1) / kBwdTile
 
 int backward_slots(int64_t batch) {
   return static_cast<int>(std::min<int64_t>(backward_tiles(batch), kMaxSlots));
+}
+
+// Persistent grid of the gradient kernel: one workgroup per CU, at most one per slot.
+// FUSED_HOAD_BWD_BLOCKS caps it, as in the reference (fused_backward.cu:873-880). Here it
+// changes only which workgroup computes a slot, never the arithmetic, so gradients stay
+// bitwise identical.
+int backward_grid(int64_t batch, int* grid) {
+  int cus = 0;
+  if (int st = current_device_cus(&cus)) return st;
+  *grid = std::min(backward_slots(batch), cus);
+  if (const char* env = std::getenv("FUSED_HOAD_BWD_BLOCKS")) {
+    const long cap = std::atol(env);
+    if (cap > 0) *grid = static_cast<int>(std::min<long>(*grid, cap));
+  }
+  return FHOAD_SUCCESS;
 }
 
 }  // namespace
@@ -996,25 +1125,55 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
     return fail(FHOAD_ERROR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes,
                 needed);
   }
-  int cus = 0;
-  if (int st = current_device_cus(&cus)) return st;
-  const int64_t tiles = backward_tiles(batch);
+  int grid = 0;
+  if (int st = backward_grid(batch, &grid)) return st;
   const int slots = backward_slots(batch);
-  int grid = std::min(slots, cus);
-  // FUSED_HOAD_BWD_BLOCKS caps the persistent grid, as in the reference
-  // (fused_backward.cu:873-880). Here it changes only which workgroup computes a slot, never
-  // the arithmetic, so gradients stay bitwise identical.
-  if (const char* env = std::getenv("FUSED_HOAD_BWD_BLOCKS")) {
-    const long cap = std::atol(env);
-    if (cap > 0) grid = static_cast<int>(std::min<long>(grid, cap));
-  }
   float* partials = static_cast<float*>(workspace);
   f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
-  hipLaunchKernelGGL(backward_kernel, dim3(grid), dim3(kBwdWaves * kWave), 0, hs, coordinates,
-                     parameters, grad_output, grad_laplacian, grad_coordinates, partials, stash,
-                     batch, tiles, slots);
+  hipLaunchKernelGGL(backward_kernel<false>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
+                     coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
+                     partials, stash, batch, backward_tiles(batch), slots, LossSeed{});
   if (int st = check_launch("backward_kernel")) return st;
   hipLaunchKernelGGL(reduce_partials_kernel, dim3((kParameterCount + 63) / 64),
                      dim3(kReduceGroups * 64), 0, hs, partials, slots, grad_parameters);
   return check_launch("reduce_partials_kernel");
+}
+
+extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* source,
+                                       float* parameters, float* exp_avg, float* exp_avg_sq,
+                                       float* step, float* loss, float* grad_parameters,
+                                       float* grad_coordinates, void* workspace,
+                                       size_t workspace_bytes, int64_t batch, double lr,
+                                       double beta1, double beta2, double eps,
+                                       double weight_decay, void* stream) {
+  if (batch <= 0) return fail(FHOAD_ERROR_INVALID_VALUE, "batch must be positive");
+  if (!coordinates || !source || !parameters || !exp_avg || !exp_avg_sq || !step || !loss) {
+    return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
+  }
+  if (!(lr >= 0.0) || !(eps >= 0.0) || !(beta1 >= 0.0 && beta1 < 1.0) ||
+      !(beta2 >= 0.0 && beta2 < 1.0) || !(weight_decay >= 0.0)) {
+    return fail(FHOAD_ERROR_INVALID_VALUE,
+                "Adam needs lr >= 0, eps >= 0, 0 <= betas < 1 and weight_decay >= 0");
+  }
+  const size_t needed = fhoad_backward_workspace_size(batch);
+  if (!workspace || workspace_bytes < needed) {
+    return fail(FHOAD_ERROR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes,
+                needed);
+  }
+  int grid = 0;
+  if (int st = backward_grid(batch, &grid)) return st;
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  const int slots = backward_slots(batch);
+  const float inv_batch = 1.0f / static_cast<float>(batch);
+  float* partials = static_cast<float*>(workspace);
+  f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
+  hipLaunchKernelGGL(backward_kernel<true>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
+                     coordinates, parameters, nullptr, nullptr, grad_coordinates, partials, stash,
+                     batch, backward_tiles(batch), slots, LossSeed{source, inv_batch, step});
+  if (int st = check_launch("backward_kernel")) return st;
+  AdamArgs args{parameters, exp_avg, exp_avg_sq, step, loss, grad_parameters,
+                lr, beta1, beta2, eps, weight_decay, inv_batch};
+  hipLaunchKernelGGL(reduce_adam_kernel, dim3((kLossColumn + 1 + 63) / 64),
+                     dim3(kReduceGroups * 64), 0, hs, partials, slots, args);
+  return check_launch("reduce_adam_kernel");
 }

@@ -68,3 +68,37 @@ def fused_forward_laplacian_backward(
         version,
     )
     return grad_parameters, grad_coordinates
+
+
+def poisson_adam_step(
+    coordinates: Tensor,
+    source: Tensor,
+    parameters: Tensor,
+    exp_avg: Tensor,
+    exp_avg_sq: Tensor,
+    step: Tensor,
+    *,
+    lr: float,
+    betas: tuple[float, float],
+    eps: float,
+    weight_decay: float,
+    grad_parameters: Tensor | None = None,
+    grad_coordinates: Tensor | None = None,
+) -> Tensor:
+    """One fused Poisson-loss + Adam step (two gfx950 kernels); updates ``parameters``,
+    ``exp_avg``, ``exp_avg_sq`` and ``step`` in place and returns the loss at entry."""
+    return load_extension().poisson_adam_step(
+        coordinates,
+        source,
+        parameters,
+        exp_avg,
+        exp_avg_sq,
+        step,
+        float(lr),
+        float(betas[0]),
+        float(betas[1]),
+        float(eps),
+        float(weight_decay),
+        grad_parameters,
+        grad_coordinates,
+    )

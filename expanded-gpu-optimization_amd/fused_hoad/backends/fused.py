@@ -17,6 +17,7 @@ from fused_hoad._extension import fused_forward_laplacian, fused_forward_laplaci
 from fused_hoad.backends.forward_laplacian import tanh_mlp_forward_laplacian
 from fused_hoad.parameters import (
     POISSON_PARAMETER_LAYOUT,
+    flattened_poisson_parameters,
     pack_poisson_parameters,
     unpack_poisson_parameters,
 )
@@ -107,6 +108,9 @@ def _packed_parameters(model: nn.Module) -> Tensor:
     parameters: list[Tensor] = _cache["parameters"]  # type: ignore[assignment]
     if torch.is_grad_enabled() and any(p.requires_grad for p in parameters):
         return pack_poisson_parameters(model, differentiable=True)
+    flat = flattened_poisson_parameters(model)
+    if flat is not None:  # the parameters are views of a packed buffer: no copy, never stale
+        return flat
     versions = [p._version for p in parameters]
     if versions != _cache.get("versions"):
         _cache.update(versions=versions, packed=pack_poisson_parameters(model))

@@ -100,3 +100,44 @@ def unpack_poisson_parameters(parameters: Tensor) -> dict[str, Tensor]:
         views[f"{spec.name}.weight"] = weight.view(spec.out_features, spec.in_features)
         views[f"{spec.name}.bias"] = parameters[spec.bias_offset : spec.end_offset]
     return views
+
+
+def flatten_poisson_parameters_(model: nn.Module) -> Tensor:
+    """Move the model's parameters into one packed ABI buffer, in place, and return it.
+
+    Each ``weight`` / ``bias`` becomes a view of the returned buffer (still a leaf
+    ``nn.Parameter``), so the model, any optimizer over ``model.parameters()`` and the fused
+    kernels all see the same memory and the pack costs nothing afterwards. Calling it again
+    on a flattened model returns the same buffer; after ``model.to(...)`` or a reassigned
+    parameter it flattens anew.
+    """
+    existing = flattened_poisson_parameters(model)
+    if existing is not None:
+        return existing
+    flat = pack_poisson_parameters(model)
+    with torch.no_grad():
+        for layer, spec in zip(_linear_layers(model), POISSON_PARAMETER_LAYOUT, strict=True):
+            layer.weight.data = flat[spec.weight_offset : spec.bias_offset].view(
+                spec.out_features, spec.in_features
+            )
+            layer.bias.data = flat[spec.bias_offset : spec.end_offset]
+    model._fused_hoad_packed = flat
+    return flat
+
+
+def flattened_poisson_parameters(model: nn.Module) -> Tensor | None:
+    """The packed buffer the model's parameters are views of, or ``None`` if they are not
+    (never flattened, moved, or a parameter reassigned since)."""
+    flat = getattr(model, "_fused_hoad_packed", None)
+    if flat is None:
+        return None
+    base = flat.data_ptr()
+    item = flat.element_size()
+    for layer, spec in zip(_linear_layers(model), POISSON_PARAMETER_LAYOUT, strict=True):
+        if (
+            layer.weight.data_ptr() != base + item * spec.weight_offset
+            or layer.bias.data_ptr() != base + item * spec.bias_offset
+            or layer.weight.device != flat.device
+        ):
+            return None
+    return flat

@@ -33,7 +33,7 @@ typedef enum fhoad_status {
   FHOAD_SUCCESS = 0,
   FHOAD_ERROR_INVALID_VERSION = 1,   /* version outside the accepted range */
   FHOAD_ERROR_INVALID_VALUE = 2,     /* null pointer or negative batch */
-  FHOAD_ERROR_MISALIGNED = 3,        /* parameters not 16-byte aligned (backward) */
+  FHOAD_ERROR_MISALIGNED = 3,        /* reserved: no entry point requires more than float alignment */
   FHOAD_ERROR_WORKSPACE = 4,         /* workspace missing or smaller than required */
   FHOAD_ERROR_DEVICE = 5             /* the HIP runtime reported an error */
 } fhoad_status;
@@ -72,7 +72,7 @@ size_t fhoad_backward_workspace_size(int64_t batch);
  * Backward of the forward Laplacian. Given dLoss/du (grad_output[batch]) and
  * dLoss/dLaplacian (grad_laplacian[batch]), writes dLoss/dparameters (grad_parameters[12737],
  * overwritten, not accumulated) and dLoss/dcoordinates (grad_coordinates[batch][2]).
- * parameters must be 16-byte aligned. workspace must hold
+ * workspace must hold
  * fhoad_backward_workspace_size(batch) bytes (its contents on entry are ignored). The
  * weight-gradient sum runs in a fixed order that does not depend on the grid size, so
  * results are bitwise reproducible. version 1..6 is accepted for API compatibility and every
@@ -86,6 +86,38 @@ int fhoad_forward_laplacian_backward(const float* coordinates, const float* para
                                      float* grad_parameters, float* grad_coordinates,
                                      void* workspace, size_t workspace_bytes, int64_t batch,
                                      int version, void* stream);
+
+/*
+ * One fused training step of the Poisson PINN loss with Adam:
+ *   loss = mean_b (laplacian(x_b) - source[b])^2, then one torch.optim.Adam update
+ *   (amsgrad = False, maximize = False) of `parameters` in place.
+ * Two kernels on `stream`: the gradient kernel re-runs the forward jet, forms the residual and
+ * its adjoint seed (grad_u = 0, grad_lap = (1 / B) 2 r) in registers and walks the adjoint
+ * back; the reduction kernel sums the weight gradient in the backward's fixed order and
+ * applies Adam to each element in the same thread.
+ *   parameters, exp_avg, exp_avg_sq: [12737] each, updated in place (Adam's first and second
+ *     moments share the packed parameter layout).
+ *   step: one float, the number of Adam steps taken so far; incremented on the device, so the
+ *     call can be captured in a HIP graph and replayed.
+ *   loss: one float, written with the loss of the parameters on entry.
+ *   grad_parameters: optional [12737] copy of the summed gradient (NULL: not written).
+ *   grad_coordinates: optional [batch][2] dLoss/dcoordinates (NULL: not written).
+ *   workspace: fhoad_backward_workspace_size(batch) bytes.
+ * Results are bitwise reproducible and do not depend on the grid size. batch must be > 0
+ * (the loss of an empty batch is undefined).
+ *
+ * Replaces, as one call, the step of /root/reference/benchmarks/benchmark_training.py:41-60:
+ * fused_forward_laplacian_cuda (csrc/fused_residual.cu:587-643), the loss
+ * (lap - source).pow(2).mean() and its autograd backward (benchmark_training.py:46-48),
+ * fused_forward_laplacian_backward_cuda (csrc/fused_backward.cu:859-934), the
+ * differentiable pack (src/fused_hoad/parameters.py:77-78) and torch.optim.Adam.step
+ * (benchmark_training.py:41).
+ */
+int fhoad_poisson_adam_step(const float* coordinates, const float* source, float* parameters,
+                            float* exp_avg, float* exp_avg_sq, float* step, float* loss,
+                            float* grad_parameters, float* grad_coordinates, void* workspace,
+                            size_t workspace_bytes, int64_t batch, double lr, double beta1,
+                            double beta2, double eps, double weight_decay, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

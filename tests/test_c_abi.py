@@ -34,6 +34,9 @@ def _lib() -> ctypes.CDLL:
     lib.fhoad_forward_laplacian.argtypes = [vp, vp, vp, vp, i64, ci, vp]
     lib.fhoad_forward_laplacian_backward.restype = ci
     lib.fhoad_forward_laplacian_backward.argtypes = [vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, i64, ci, vp]
+    d = ctypes.c_double
+    lib.fhoad_poisson_adam_step.restype = ci
+    lib.fhoad_poisson_adam_step.argtypes = [vp] * 10 + [ctypes.c_size_t, i64, d, d, d, d, d, vp]
     return lib
 
 
@@ -50,6 +53,7 @@ def test_header_declares_the_entry_points() -> None:
         "fhoad_forward_laplacian_backward",
         "fhoad_last_error",
         "fhoad_parameter_count",
+        "fhoad_poisson_adam_step",
         "fhoad_status_string",
     ]
 
@@ -89,6 +93,17 @@ def test_argument_errors_are_reported_before_any_device_work() -> None:
     assert lib.fhoad_forward_laplacian_backward(None, None, None, None, None, None, None, 0, 4, 0, None) == 1
     assert b"backward version must be 1 to 6" in lib.fhoad_last_error()
     assert lib.fhoad_forward_laplacian_backward(None, None, None, None, None, None, None, 0, -3, 6, None) == 2
+    step = lib.fhoad_poisson_adam_step
+    assert step(*[None] * 10, 0, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0, None) == 2
+    assert b"batch must be positive" in lib.fhoad_last_error()
+    assert step(*[None] * 10, 0, 16, 1e-3, 0.9, 0.999, 1e-8, 0.0, None) == 2
+    assert b"null device pointer" in lib.fhoad_last_error()
+    # Dummy non-null addresses: the argument checks fail before anything is dereferenced.
+    fake = [ctypes.c_void_p(256)] * 7 + [None, None, ctypes.c_void_p(256)]
+    assert step(*fake, 1 << 30, 16, 1e-3, 1.0, 0.999, 1e-8, 0.0, None) == 2
+    assert b"betas" in lib.fhoad_last_error()
+    assert step(*fake, 1 << 30, 16, -1e-3, 0.9, 0.999, 1e-8, 0.0, None) == 2
+    assert step(*fake, 10, 16, 1e-3, 0.9, 0.999, 1e-8, 0.0, None) == 4
 
 
 def test_torch_extension_reports_contract_errors_on_cpu() -> None:
@@ -143,3 +158,45 @@ def test_raw_entry_points_match_the_torch_extension() -> None:
         x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), gp.data_ptr(), gx.data_ptr(),
         ws.data_ptr(), ws_bytes - 1, batch, 6, stream)
     assert status == 4
+
+
+@pytest.mark.gpu
+def test_raw_fused_step_matches_the_torch_extension() -> None:
+    from gpu_helpers import announce, coordinates, packed, require_gpu_extension
+
+    require_gpu_extension()
+    announce("C ABI fhoad_poisson_adam_step via ctypes vs fused_hoad._C, batch=3000")
+    from fused_hoad import _C, manufactured_source
+
+    lib = _lib()
+    batch = 3000
+    x = coordinates(batch, seed=13)
+    f = manufactured_source(x).reshape(-1).contiguous()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def state():
+        p = packed(0)
+        return p, torch.zeros_like(p), torch.zeros_like(p), torch.zeros(1, device="cuda")
+
+    p, m, v, t = state()
+    loss = torch.empty((), device="cuda")
+    gp = torch.empty(12737, device="cuda")
+    gx = torch.empty(batch, 2, device="cuda")
+    ws_bytes = lib.fhoad_backward_workspace_size(batch)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        status = lib.fhoad_poisson_adam_step(
+            x.data_ptr(), f.data_ptr(), p.data_ptr(), m.data_ptr(), v.data_ptr(), t.data_ptr(),
+            loss.data_ptr(), gp.data_ptr(), gx.data_ptr(), ws.data_ptr(), ws_bytes, batch,
+            1e-3, 0.9, 0.999, 1e-8, 0.0, stream)
+        assert status == 0, lib.fhoad_last_error()
+
+    ep, em, ev, et = state()
+    egp = torch.empty_like(gp)
+    egx = torch.empty_like(gx)
+    for _ in range(2):
+        eloss = _C.poisson_adam_step(x, f, ep, em, ev, et, 1e-3, 0.9, 0.999, 1e-8, 0.0, egp, egx)
+    torch.cuda.synchronize()
+    for a, b in ((p, ep), (m, em), (v, ev), (t, et), (loss, eloss), (gp, egp), (gx, egx)):
+        assert torch.equal(a, b)
+    assert float(t) == 2.0
