@@ -393,6 +393,15 @@ __device__ __forceinline__ void layer0_forward(const float* s_small, int g, floa
   }
 }
 
+// An opaque copy of a value: the compiler cannot see that it equals the input, so it cannot
+// hoist arithmetic on it (addresses, lane masks) out of the enclosing loop and keep the results
+// live, where at full register use they would be spilled.
+template <typename T>
+__device__ __forceinline__ T opaque(T x) {
+  __asm__ volatile("" : "+v"(x));
+  return x;
+}
+
 // The small LDS parameters read per tile have loop-invariant addresses; left alone, the
 // compiler hoists those reads out of the tile loop and keeps ~100 values live in registers for
 // the whole kernel. An empty asm statement with a memory clobber at the top of each tile keeps
@@ -565,15 +574,15 @@ __device__ __forceinline__ float dw_product(const float* stage_rows, int w, f4 (
   return bias;
 }
 
-// Sum of staged plane `plane` over the 64 points for neuron 16 w + m, complete in every lane.
-__device__ __forceinline__ float plane_sum(const float* stage_rows, int plane, int w) {
-  float acc = 0.0f;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const f4 v = lds4(stage_rows + plane * kPlane + 1088 * w + 16 * s);
-    acc += (v[0] + v[1]) + (v[2] + v[3]);
-  }
-  return sum_lane_groups(acc);
+// Per-neuron sums over a wave's 16 points without LDS: lane (m, g) holds x for neuron
+// 16 mb + 4 g + r at point m, so a DPP row sum gives that neuron's total in all 16 lanes of row
+// g. Lane (m, g) keeps the total of neuron owned_neuron(m, g) = 16 (m >> 2) + 4 g + (m & 3):
+// the 64 lanes own the 64 neurons once each.
+__device__ __forceinline__ int owned_neuron(int m, int g) { return 16 * (m >> 2) + 4 * g + (m & 3); }
+
+__device__ __forceinline__ void pick_row_sum(float x, int k, int m, float& keep) {
+  const float total = sum_row16(x);
+  keep = (m == k) ? total : keep;
 }
 
 // Replace a hidden layer's pre-activation z by its adjoint zbar, given the adjoint hb of the
@@ -688,11 +697,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   const int w = threadIdx.x / kWave;
   const int m = lane & 15;
   const int g = lane >> 4;
-  const float* w_rows = s_w + lane_rows(m, g);
-  const float* w_cols = s_w + lane_cols(m, g);
-  float* stage_lane = s_stage + lane_cols(m, g) + 16 * w;
+  // Lane offsets into the LDS arrays. Each use forms its base from an opaque copy: the arrays
+  // span more than the 64 KB reach of a DS offset, and hoisted bases would be spilled.
+  const int rows_off = lane_rows(m, g);
+  const int cols_off = lane_cols(m, g);
+  const int stage_lane_off = cols_off + 16 * w;
   f4* my_stash = stash + static_cast<int64_t>(blockIdx.x * kBwdWaves + w) * kStashF4PerWave + lane;
-  const float* stage_rows = s_stage + lane_rows(m, g);
 
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
     f4 dw[3][4];
@@ -707,6 +717,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 
     for (int64_t tile = slot; tile < tiles; tile += slots) {
       keep_lds_reads_in_loop();
+      const int m_pick = opaque(m);  // pick_row_sum's 16 lane masks stay inside the tile
       const int64_t point = tile * kBwdTile + kTile * w + m;
       const bool active = point < batch;
       float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f, f = 0.f;
@@ -727,18 +738,19 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       layer0_forward(s_small, g, x0, x1, h);
       {
         f4 z1[4][4];
-        hidden_layer(s_small, w_rows, 0, g, h, z1);
+        hidden_layer(s_small, s_w + opaque(rows_off), 0, g, h, z1);
+        f4* stash_st = opaque(my_stash);
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) my_stash[(4 * mb + c) * kWave] = z1[mb][c];
+          for (int c = 0; c < 4; ++c) stash_st[(4 * mb + c) * kWave] = z1[mb][c];
         }
         keep_lds_reads_in_loop();  // issue the stores here, so z1 is not held until later
         apply_tanh_jet(z1, h);
       }
-      hidden_layer(s_small, w_rows, 1, g, h, z2);
+      hidden_layer(s_small, s_w + opaque(rows_off), 1, g, h, z2);
       apply_tanh_jet(z2, h);
-      hidden_layer(s_small, w_rows, 2, g, h, z3);
+      hidden_layer(s_small, s_w + opaque(rows_off), 2, g, h, z3);
       f4 tv[4], ts[4];  // (v', s) of the layer whose adjoint comes next
       apply_tanh_jet_vs(z3, h, tv, ts);
 
@@ -758,125 +770,132 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       }
 
       // ---- 2. output layer: w_out / b_out gradients and the adjoint seed ----
-      __syncthreads();  // the staging buffer is free
       // In the scaled jet u = (w_out / c) . v' and lap = (w_out / lambda) . L', so
       // dw_out = sum_p (gu / c) v' + (gl / lambda) L' and the seeds are vbar' = gu w_out / c,
-      // Lbar' = gl w_out / lambda, Jbar = 0.
+      // Lbar' = gl w_out / lambda, Jbar = 0. The point sums stay in registers (pick_row_sum).
       f4 hb[4][4];
-      const float gu_c = gu * (1.0f / kC);
-      const float gl_l = gl * (1.0f / kLambda);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
-        const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          stage_lane[1088 * mb + kWRow * r] = __builtin_fmaf(gu_c, h[mb][0][r], gl_l * h[mb][3][r]);
-          hb[mb][0][r] = gu * wv[r];
-          hb[mb][1][r] = 0.0f;
-          hb[mb][2][r] = 0.0f;
-          hb[mb][3][r] = gl * wl[r];
-        }
-      }
       {
-        const float su = sum_row16(gu);
-        if (lane == 0) s_red[w] = su;
+        const float gu_c = gu * (1.0f / kC);
+        const float gl_l = gl * (1.0f / kLambda);
+        float wout_sum = 0.0f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+          const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            pick_row_sum(__builtin_fmaf(gu_c, h[mb][0][r], gl_l * h[mb][3][r]), 4 * mb + r, m_pick,
+                         wout_sum);
+            hb[mb][0][r] = gu * wv[r];
+            hb[mb][1][r] = 0.0f;
+            hb[mb][2][r] = 0.0f;
+            hb[mb][3][r] = gl * wl[r];
+          }
+        }
+        g_wout += wout_sum;
+        if (!kLoss) g_bout += sum_row16(gu);
       }
-      __syncthreads();
-      g_wout += plane_sum(stage_rows, 0, w);
-      g_bout += ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
 
       // ---- 3. hidden layer 3 ----
       tanh_adjoint_in_place(z3, hb, tv, ts);
-      stage_and_dw<false>(z3, z2, dw[2], g_bh[2], stage_lane, stage_rows, s_small, w, g, x0, x1,
+      stage_and_dw<false>(z3, z2, dw[2], g_bh[2], s_stage + opaque(stage_lane_off),
+                          s_stage + opaque(rows_off), s_small, w, g, x0, x1,
                           tv, ts);
-      hidden_product_t(w_cols + 2 * kPlane, z3, hb);
+      hidden_product_t(s_w + opaque(cols_off) + 2 * kPlane, z3, hb);
 
       // ---- 4. hidden layer 2 (needs hidden layer 1's z back from the stash) ----
       keep_lds_reads_in_loop();  // the reload below must read memory, not forward the stores
+      const f4* stash_ld = opaque(my_stash);
       f4 z1[4][4];
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) z1[mb][c] = my_stash[(4 * mb + c) * kWave];
+        for (int c = 0; c < 4; ++c) z1[mb][c] = stash_ld[(4 * mb + c) * kWave];
       }
       tanh_adjoint_in_place(z2, hb, tv, ts);
-      stage_and_dw<false>(z2, z1, dw[1], g_bh[1], stage_lane, stage_rows, s_small, w, g, x0, x1,
+      stage_and_dw<false>(z2, z1, dw[1], g_bh[1], s_stage + opaque(stage_lane_off),
+                          s_stage + opaque(rows_off), s_small, w, g, x0, x1,
                           tv, ts);
-      hidden_product_t(w_cols + kPlane, z2, hb);
+      hidden_product_t(s_w + opaque(cols_off) + kPlane, z2, hb);
 
       // ---- 5. hidden layer 1 ----
       tanh_adjoint_in_place(z1, hb, tv, ts);
-      stage_and_dw<true>(z1, z1, dw[0], g_bh[0], stage_lane, stage_rows, s_small, w, g, x0, x1,
+      stage_and_dw<true>(z1, z1, dw[0], g_bh[0], s_stage + opaque(stage_lane_off),
+                          s_stage + opaque(rows_off), s_small, w, g, x0, x1,
                          tv, ts);
-      hidden_product_t(w_cols, z1, hb);
+      hidden_product_t(s_w + opaque(cols_off), z1, hb);
 
       // ---- 6. layer 0 in closed form ----
       // bv is the adjoint of c z_v, so zbar_v = c bv: grad_x = (c W0)^T bv,
       // dW0[o][d] = sum_p bv (c x_d) + zbar_Jd, db0 = c sum_p bv.
-      float gx0 = 0.f, gx1 = 0.f;
-      const float cx0 = kC * x0, cx1 = kC * x1;
-      __syncthreads();  // staging buffer free again
+      {
+        float gx0 = 0.f, gx1 = 0.f, w0x_sum = 0.f, w0y_sum = 0.f, b0_sum = 0.f;
+        const float cx0 = kC * x0, cx1 = kC * x1;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const Layer0Weights w0 = layer0_weights(s_small, mb, g);
+        for (int mb = 0; mb < 4; ++mb) {
+          const Layer0Weights w0 = layer0_weights(s_small, mb, g);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float bv = hb[mb][0][r], bj0 = hb[mb][1][r], bj1 = hb[mb][2][r], bl = hb[mb][3][r];
-          tanh_jet_adjoint_vs(tv[mb][r], ts[mb][r], w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
-          gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
-          gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
-          float* p = stage_lane + 1088 * mb + kWRow * r;
-          p[0] = __builtin_fmaf(bv, cx0, bj0);       // dW0[o][0] contribution
-          p[kPlane] = __builtin_fmaf(bv, cx1, bj1);  // dW0[o][1]
-          p[2 * kPlane] = bv;                        // db0[o] / c
+          for (int r = 0; r < 4; ++r) {
+            float bv = hb[mb][0][r], bj0 = hb[mb][1][r], bj1 = hb[mb][2][r], bl = hb[mb][3][r];
+            tanh_jet_adjoint_vs(tv[mb][r], ts[mb][r], w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
+            gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
+            gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
+            pick_row_sum(__builtin_fmaf(bv, cx0, bj0), 4 * mb + r, m_pick, w0x_sum);  // dW0[o][0]
+            pick_row_sum(__builtin_fmaf(bv, cx1, bj1), 4 * mb + r, m_pick, w0y_sum);  // dW0[o][1]
+            pick_row_sum(bv, 4 * mb + r, m_pick, b0_sum);                              // db0[o] / c
+          }
+        }
+        g_w0x += w0x_sum;
+        g_w0y += w0y_sum;
+        g_b0 += b0_sum;
+        gx0 = sum_lane_groups(gx0);
+        gx1 = sum_lane_groups(gx1);
+        if (g == 0 && active && (!kLoss || grad_coordinates != nullptr)) {
+          grad_coordinates[2 * point] = gx0;
+          grad_coordinates[2 * point + 1] = gx1;
         }
       }
-      gx0 = sum_lane_groups(gx0);
-      gx1 = sum_lane_groups(gx1);
-      if (g == 0 && active && (!kLoss || grad_coordinates != nullptr)) {
-        grad_coordinates[2 * point] = gx0;
-        grad_coordinates[2 * point + 1] = gx1;
-      }
-      __syncthreads();
-      g_w0x += plane_sum(stage_rows, 0, w);
-      g_w0y += plane_sum(stage_rows, 1, w);
-      g_b0 += plane_sum(stage_rows, 2, w);
     }
 
     // ---- this slot's partial row: every entry written by exactly one lane ----
     float* row = partials + static_cast<int64_t>(slot) * kRowStride;
+    const int dw_lane = opaque((16 * w + 4 * g) * kHidden + m);
 #pragma unroll
     for (int l = 0; l < 3; ++l) {
       float* wrow = row + kHiddenBase + l * kHiddenStride;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wrow[(16 * w + 4 * g + r) * kHidden + 16 * nb + m] = dw[l][nb][r];
+        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = dw[l][nb][r];
       }
       if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * g_bh[l];  // bias sums are of c^-1 zbar_v
     }
-    if (g == 0) {
-      const int o = 16 * w + m;
-      row[kInputs * o] = g_w0x;
-      row[kInputs * o + 1] = g_w0y;
-      row[kLayer0Bias + o] = kC * g_b0;
-      row[kOutputBase + o] = g_wout;
-    }
-    if (threadIdx.x == 0) row[kOutputBase + kHidden] = g_bout;
-    if (kLoss) {
-      __syncthreads();  // every wave is done with s_red
-      if (lane == 0) s_red[w] = g_loss;
+    // Per-wave sums (lane = owned neuron) combined over the 4 waves in a fixed order.
+    __syncthreads();  // every wave is done with the staging buffer
+    {
+      float* comb = s_stage;  // [quantity][wave][neuron]
+      const int o = owned_neuron(m, g);
+      comb[(0 * kBwdWaves + w) * kHidden + o] = g_w0x;
+      comb[(1 * kBwdWaves + w) * kHidden + o] = g_w0y;
+      comb[(2 * kBwdWaves + w) * kHidden + o] = g_b0;
+      comb[(3 * kBwdWaves + w) * kHidden + o] = g_wout;
+      if (lane == 0) s_red[w] = kLoss ? g_loss : g_bout;
       __syncthreads();
-      if (threadIdx.x == 0) row[kLossColumn] = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
+      const int q = threadIdx.x >> 6, n = threadIdx.x & 63;  // quantity (0..3), neuron
+      const float* c4 = comb + q * kBwdWaves * kHidden + n;
+      const float total = ((c4[0] + c4[kHidden]) + c4[2 * kHidden]) + c4[3 * kHidden];
+      const int dst = q == 0 ? kInputs * n : q == 1 ? kInputs * n + 1 : q == 2 ? kLayer0Bias + n : kOutputBase + n;
+      row[dst] = q == 2 ? kC * total : total;
+      if (threadIdx.x == 0) {
+        const float red = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
+        row[kOutputBase + kHidden] = kLoss ? 0.0f : red;
+        if (kLoss) row[kLossColumn] = red;
+      }
     }
     __syncthreads();  // s_red and the staging buffer are reused by the next slot
   }
 }
 
-// grad[k] = sum over slots of partials[slot][k], in a fixed tree: 16 groups of 16 consecutive
-// slots are summed in slot order, then the 16 group sums in group order. Slots at or beyond
-// `slots` are skipped (they would add +0.0f).
 // Column k's total over the slots, complete in the threads of group 0 (columns >= `columns`
 // read nothing and give 0).
 __device__ __forceinline__ float fixed_tree_sum(const float* __restrict__ partials, int slots,
@@ -904,6 +923,9 @@ __device__ __forceinline__ float fixed_tree_sum(const float* __restrict__ partia
   return total;
 }
 
+// grad[k] = sum over slots of partials[slot][k], in a fixed tree: 16 groups of 16 consecutive
+// slots are summed in slot order, then the 16 group sums in group order. Slots at or beyond
+// `slots` are skipped (they would add +0.0f).
 __global__ void __launch_bounds__(kReduceGroups * 64)
 reduce_partials_kernel(const float* __restrict__ partials, int slots, float* __restrict__ grad) {
   __shared__ float s_part[kReduceGroups][64];
