@@ -97,17 +97,18 @@ std::vector<torch::Tensor> fused_forward_laplacian_backward(torch::Tensor coordi
   return {grad_parameters, grad_coordinates};
 }
 
-// One fused Poisson + Adam training step (fhoad_poisson_adam_step). No counterpart among the
-// reference's bindings: it replaces the Python step of
-// /root/reference/benchmarks/benchmark_training.py:41-60 (fused forward, loss, fused backward,
-// torch.optim.Adam). parameters, exp_avg, exp_avg_sq and step are updated in place; returns the
-// loss (a 0-dim tensor) of the parameters on entry.
+// One fused Poisson PINN + Adam training step (fhoad_poisson_adam_step). No counterpart among
+// the reference's bindings: it replaces the Python step of
+// /root/reference/benchmarks/train_poisson.py:30-45 and benchmark_training.py:41-60 (fused
+// forward, loss, fused backward, torch.optim.Adam). parameters, exp_avg, exp_avg_sq and step
+// are updated in place; returns the loss (a 0-dim tensor) of the parameters on entry.
 torch::Tensor poisson_adam_step(torch::Tensor coordinates, torch::Tensor source,
                                 torch::Tensor parameters, torch::Tensor exp_avg,
                                 torch::Tensor exp_avg_sq, torch::Tensor step, double lr,
                                 double beta1, double beta2, double eps, double weight_decay,
                                 c10::optional<torch::Tensor> grad_parameters,
-                                c10::optional<torch::Tensor> grad_coordinates) {
+                                c10::optional<torch::Tensor> grad_coordinates,
+                                c10::optional<torch::Tensor> boundary, double boundary_weight) {
   check_inputs(coordinates, parameters);
   const int64_t batch = coordinates.size(0);
   TORCH_CHECK(batch > 0, "coordinates must hold at least one point");
@@ -123,6 +124,8 @@ torch::Tensor poisson_adam_step(torch::Tensor coordinates, torch::Tensor source,
   check_like(step, 1, "step");
   float* grad_parameters_ptr = nullptr;
   float* grad_coordinates_ptr = nullptr;
+  const float* boundary_ptr = nullptr;
+  int64_t boundary_count = 0;
   if (grad_parameters.has_value()) {
     check_like(*grad_parameters, kParameterCount, "grad_parameters");
     grad_parameters_ptr = grad_parameters->data_ptr<float>();
@@ -131,28 +134,39 @@ torch::Tensor poisson_adam_step(torch::Tensor coordinates, torch::Tensor source,
     check_like(*grad_coordinates, 2 * batch, "grad_coordinates");
     grad_coordinates_ptr = grad_coordinates->data_ptr<float>();
   }
+  if (boundary.has_value()) {
+    TORCH_CHECK(boundary->dim() == 2 && boundary->size(1) == 2,
+                "boundary must have shape [count, 2]");
+    boundary_count = boundary->size(0);
+    check_like(*boundary, 2 * boundary_count, "boundary");
+    boundary_ptr = boundary->data_ptr<float>();
+  }
+  TORCH_CHECK(boundary_weight >= 0.0, "boundary_weight must be non-negative");
   const c10::DeviceGuard device_guard(coordinates.device());
   auto loss = torch::empty({}, coordinates.options());
-  const size_t workspace_bytes = fhoad_backward_workspace_size(batch);
+  const size_t workspace_bytes = fhoad_poisson_adam_step_workspace_size(batch, boundary_count);
   auto workspace = torch::empty({static_cast<int64_t>(workspace_bytes)},
                                 coordinates.options().dtype(torch::kUInt8));
   check_status(fhoad_poisson_adam_step(
-      coordinates.data_ptr<float>(), source.data_ptr<float>(), parameters.data_ptr<float>(),
-      exp_avg.data_ptr<float>(), exp_avg_sq.data_ptr<float>(), step.data_ptr<float>(),
-      loss.data_ptr<float>(), grad_parameters_ptr, grad_coordinates_ptr, workspace.data_ptr(),
-      workspace_bytes, batch, lr, beta1, beta2, eps, weight_decay, current_stream(coordinates)));
+      coordinates.data_ptr<float>(), source.data_ptr<float>(), batch, boundary_ptr,
+      boundary_count, boundary_weight, parameters.data_ptr<float>(), exp_avg.data_ptr<float>(),
+      exp_avg_sq.data_ptr<float>(), step.data_ptr<float>(), loss.data_ptr<float>(),
+      grad_parameters_ptr, grad_coordinates_ptr, workspace.data_ptr(), workspace_bytes, lr, beta1,
+      beta2, eps, weight_decay, current_stream(coordinates)));
   return loss;
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
   module.def("poisson_adam_step", &poisson_adam_step,
-             "Fused Poisson-loss training step with Adam on the packed parameters (MI355X)",
+             "Fused Poisson PINN training step with Adam on the packed parameters (MI355X)",
              pybind11::arg("coordinates"), pybind11::arg("source"), pybind11::arg("parameters"),
              pybind11::arg("exp_avg"), pybind11::arg("exp_avg_sq"), pybind11::arg("step"),
              pybind11::arg("lr"), pybind11::arg("beta1"), pybind11::arg("beta2"),
              pybind11::arg("eps"), pybind11::arg("weight_decay"),
              pybind11::arg("grad_parameters") = pybind11::none(),
-             pybind11::arg("grad_coordinates") = pybind11::none());
+             pybind11::arg("grad_coordinates") = pybind11::none(),
+             pybind11::arg("boundary") = pybind11::none(),
+             pybind11::arg("boundary_weight") = 100.0);
   module.def("fused_forward_laplacian", &fused_forward_laplacian,
              "Fixed MLP forward pass and input Laplacian (MI355X HIP kernel)",
              pybind11::arg("coordinates"), pybind11::arg("parameters"),

@@ -656,21 +656,29 @@ __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&
   dw_product(stage_rows, w, dw);
 }
 
-// Seed of the fused Poisson training step (kLoss): the loss is mean((lap - f)^2) over the
-// batch, so the backward needs grad_u = 0 and grad_lap = (1 / B) (2 r) with r = lap - f,
-// exactly the upstream gradients autograd forms for (lap - f).pow(2).mean()
-// (/root/reference/benchmarks/benchmark_training.py:46-48). The kernel already re-runs the
-// forward, so it forms lap, r and the seed itself; sum r^2 goes into column kLossColumn of the
-// slot's partial row. `step` is the Adam step counter, advanced here (one lane of workgroup 0)
-// so that the update kernel that follows reads a settled value.
+// Seed of the fused Poisson training step (kLoss). The loss is the PINN loss
+//   mean_interior (lap - f)^2 + w mean_boundary u^2
+// (/root/reference/src/fused_hoad/training.py:66-88; with no boundary points, the loss of
+// /root/reference/benchmarks/benchmark_training.py:46-48). The kernel already re-runs the
+// forward, so it forms the upstream gradients autograd would form for that loss itself:
+//   interior points: grad_u = 0, grad_lap = fl(1 / B) (2 r) with r = lap - f;
+//   boundary points: grad_u = fl(w / B_b) (2 u), grad_lap = 0.
+// Tiles [0, interior_tiles) hold interior points and the rest boundary points. sum r^2 and
+// sum u^2 go into columns kLossColumn and kLossColumn + 1 of the slot's partial row. `step` is
+// the Adam step counter, advanced here (one lane of workgroup 0) so that the update kernel that
+// follows reads a settled value.
 struct LossSeed {
-  const float* source;  // f[batch]
-  float inv_batch;      // fl(1 / B)
-  float* step;          // Adam step counter (one float)
+  const float* source;     // f[batch]
+  const float* boundary;   // boundary coordinates [boundary_count][2]
+  int64_t interior_tiles;  // ceil(batch / 64)
+  int64_t boundary_count;
+  float inv_batch;         // fl(1 / B)
+  float boundary_scale;    // fl(fl(w) / B_b)
+  float* step;             // Adam step counter (one float)
 };
 
-constexpr int kLossColumn = kParameterCount;  // partial-row column of sum r^2
-static_assert(kLossColumn < kRowStride, "the loss column must fit in a partial row");
+constexpr int kLossColumn = kParameterCount;  // partial-row columns of sum r^2, sum u_b^2
+static_assert(kLossColumn + 1 < kRowStride, "the loss columns must fit in a partial row");
 
 // z of hidden layers 2 and 3 stays in registers through the walk back; z of hidden layer 1
 // would push the live state past the register file, so each wave parks it in its own 16 KB
@@ -688,7 +696,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ __attribute__((aligned(16))) float s_stage[4 * kPlane];
-  __shared__ float s_red[kBwdWaves];
+  __shared__ float s_red[3][kBwdWaves];
   if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] += 1.0f;
   stage_parameters<kBwdWaves * kWave>(params, s_w, s_small, threadIdx.x);
   __syncthreads();
@@ -713,19 +721,21 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     }
     float g_bh[3] = {0.f, 0.f, 0.f};
     float g_w0x = 0.f, g_w0y = 0.f, g_b0 = 0.f, g_wout = 0.f, g_bout = 0.f;
-    float g_loss = 0.f;  // kLoss: this wave's sum of r^2 over the slot's tiles
+    float g_loss = 0.f, g_bloss = 0.f;  // kLoss: this wave's sums of r^2 and u_b^2
 
     for (int64_t tile = slot; tile < tiles; tile += slots) {
       keep_lds_reads_in_loop();
       const int m_pick = opaque(m);  // pick_row_sum's 16 lane masks stay inside the tile
-      const int64_t point = tile * kBwdTile + kTile * w + m;
-      const bool active = point < batch;
+      const bool on_boundary = kLoss && tile >= seed.interior_tiles;  // uniform per tile
+      const int64_t point = (on_boundary ? tile - seed.interior_tiles : tile) * kBwdTile + kTile * w + m;
+      const bool active = point < (on_boundary ? seed.boundary_count : batch);
+      const float* xy = on_boundary ? seed.boundary : coordinates;
       float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f, f = 0.f;
       if (active) {
-        x0 = coordinates[2 * point];
-        x1 = coordinates[2 * point + 1];
+        x0 = xy[2 * point];
+        x1 = xy[2 * point + 1];
         if (kLoss) {
-          f = seed.source[point];
+          if (!on_boundary) f = seed.source[point];
         } else {
           gu = grad_output[point];
           gl = grad_laplacian[point];
@@ -755,18 +765,27 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       apply_tanh_jet_vs(z3, h, tv, ts);
 
       if (kLoss) {
-        // lap = w_out . L in the forward kernel's order, then the residual seed.
-        float lap = 0.0f;
+        // u = w_out . v + b_out (boundary) or lap = w_out . L (interior), in the forward
+        // kernel's order, then the seed.
+        float out = 0.0f;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-          const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
+          const f4 wo = lds4(s_small + (on_boundary ? kSmallWoutV : kSmallWoutL) + 16 * mb + 4 * g);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) lap = __builtin_fmaf(wl[r], h[mb][3][r], lap);
+          for (int r = 0; r < 4; ++r) {
+            out = __builtin_fmaf(wo[r], on_boundary ? h[mb][0][r] : h[mb][3][r], out);
+          }
         }
-        lap = sum_lane_groups(lap);
-        const float res = active ? lap - f : 0.0f;
-        gl = seed.inv_batch * (2.0f * res);
-        g_loss += sum_row16(res * res);
+        out = sum_lane_groups(out);
+        if (on_boundary) {
+          const float u = active ? out + s_small[kSmallBout] : 0.0f;
+          gu = seed.boundary_scale * (2.0f * u);
+          g_bloss += sum_row16(u * u);
+        } else {
+          const float res = active ? out - f : 0.0f;
+          gl = seed.inv_batch * (2.0f * res);
+          g_loss += sum_row16(res * res);
+        }
       }
 
       // ---- 2. output layer: w_out / b_out gradients and the adjoint seed ----
@@ -793,7 +812,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
           }
         }
         g_wout += wout_sum;
-        if (!kLoss) g_bout += sum_row16(gu);
+        g_bout += sum_row16(gu);
       }
 
       // ---- 3. hidden layer 3 ----
@@ -850,7 +869,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         g_b0 += b0_sum;
         gx0 = sum_lane_groups(gx0);
         gx1 = sum_lane_groups(gx1);
-        if (g == 0 && active && (!kLoss || grad_coordinates != nullptr)) {
+        if (g == 0 && active && (!kLoss || (grad_coordinates != nullptr && !on_boundary))) {
           grad_coordinates[2 * point] = gx0;
           grad_coordinates[2 * point + 1] = gx1;
         }
@@ -879,17 +898,21 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       comb[(1 * kBwdWaves + w) * kHidden + o] = g_w0y;
       comb[(2 * kBwdWaves + w) * kHidden + o] = g_b0;
       comb[(3 * kBwdWaves + w) * kHidden + o] = g_wout;
-      if (lane == 0) s_red[w] = kLoss ? g_loss : g_bout;
+      if (lane == 0) {
+        s_red[0][w] = g_bout;
+        s_red[1][w] = g_loss;
+        s_red[2][w] = g_bloss;
+      }
       __syncthreads();
       const int q = threadIdx.x >> 6, n = threadIdx.x & 63;  // quantity (0..3), neuron
       const float* c4 = comb + q * kBwdWaves * kHidden + n;
       const float total = ((c4[0] + c4[kHidden]) + c4[2 * kHidden]) + c4[3 * kHidden];
       const int dst = q == 0 ? kInputs * n : q == 1 ? kInputs * n + 1 : q == 2 ? kLayer0Bias + n : kOutputBase + n;
       row[dst] = q == 2 ? kC * total : total;
-      if (threadIdx.x == 0) {
-        const float red = ((s_red[0] + s_red[1]) + s_red[2]) + s_red[3];
-        row[kOutputBase + kHidden] = kLoss ? 0.0f : red;
-        if (kLoss) row[kLossColumn] = red;
+      if (threadIdx.x < (kLoss ? 3 : 1)) {
+        const float* red = s_red[threadIdx.x];
+        const int col = threadIdx.x == 0 ? kOutputBase + kHidden : kLossColumn + threadIdx.x - 1;
+        row[col] = ((red[0] + red[1]) + red[2]) + red[3];
       }
     }
     __syncthreads();  // s_red and the staging buffer are reused by the next slot
@@ -942,10 +965,12 @@ struct AdamArgs {
   float* exp_avg;
   float* exp_avg_sq;
   const float* step;  // already advanced for this step by the gradient kernel
-  float* loss;        // mean r^2
+  float* loss;        // mean r^2 + w mean u_b^2
   float* grad;        // optional copy of the summed gradient (nullptr: none)
   double lr, beta1, beta2, eps, weight_decay;
-  float inv_batch;
+  float inv_batch;       // fl(1 / B)
+  float inv_boundary;    // fl(1 / B_b), 0 without boundary points
+  float boundary_weight; // fl(w)
 };
 
 // The fixed-tree gradient sum of reduce_partials_kernel, then the Adam update of each
@@ -953,18 +978,23 @@ struct AdamArgs {
 // arithmetic follows torch's multi-tensor Adam (torch/optim/adam.py, _multi_tensor_adam):
 //   g += wd p;  m = lerp(m, g, 1 - b1);  v = v b2 + (1 - b2) g g;
 //   p += -(lr / bc1) m / (sqrt(v) / sqrt(bc2) + eps),  bc_i = 1 - b_i^t,
-// with the bias corrections in double and every tensor operation rounded to float. Column
-// kLossColumn gives loss = inv_batch * sum r^2.
+// with the bias corrections in double and every tensor operation rounded to float. Columns
+// kLossColumn and kLossColumn + 1 give loss = fl(sum r^2 / B) + fl(w fl(sum u_b^2 / B_b)).
 __global__ void __launch_bounds__(kReduceGroups * 64)
 reduce_adam_kernel(const float* __restrict__ partials, int slots, AdamArgs a) {
   __shared__ float s_part[kReduceGroups][64];
+  __shared__ float s_loss[2];
   const int col = threadIdx.x & 63;
   const int group = threadIdx.x >> 6;
   const int k = blockIdx.x * 64 + col;
-  const float total = fixed_tree_sum(partials, slots, k, kLossColumn + 1, s_part, group, col);
+  const float total = fixed_tree_sum(partials, slots, k, kLossColumn + 2, s_part, group, col);
+  if (group == 0 && (k == kLossColumn || k == kLossColumn + 1)) s_loss[k - kLossColumn] = total;
+  __syncthreads();
   if (group != 0) return;
   if (k == kLossColumn) {
-    a.loss[0] = total * a.inv_batch;
+    const float interior = s_loss[0] * a.inv_batch;
+    a.loss[0] = a.inv_boundary != 0.0f ? interior + a.boundary_weight * (s_loss[1] * a.inv_boundary)
+                                       : interior;
     return;
   }
   if (k >= kParameterCount) return;
@@ -1046,18 +1076,25 @@ int current_device_cus(int* cus) {
 
 int64_t backward_tiles(int64_t batch) { return (batch + kBwdTile - 1) / kBwdTile; }
 
-int backward_slots(int64_t batch) {
-  return static_cast<int>(std::min<int64_t>(backward_tiles(batch), kMaxSlots));
+int slots_for_tiles(int64_t tiles) { return static_cast<int>(std::min<int64_t>(tiles, kMaxSlots)); }
+
+int backward_slots(int64_t batch) { return slots_for_tiles(backward_tiles(batch)); }
+
+// Workspace of the gradient kernel for `slots` slots: the partial rows, then one z stash per
+// (workgroup, wave); the grid never exceeds `slots`, so both are sized by it.
+size_t workspace_bytes_for(int slots) {
+  return static_cast<size_t>(slots) *
+         (kRowStride * sizeof(float) + kBwdWaves * kStashF4PerWave * sizeof(f4));
 }
 
 // Persistent grid of the gradient kernel: one workgroup per CU, at most one per slot.
 // FUSED_HOAD_BWD_BLOCKS caps it, as in the reference (fused_backward.cu:873-880). Here it
 // changes only which workgroup computes a slot, never the arithmetic, so gradients stay
 // bitwise identical.
-int backward_grid(int64_t batch, int* grid) {
+int backward_grid(int slots, int* grid) {
   int cus = 0;
   if (int st = current_device_cus(&cus)) return st;
-  *grid = std::min(backward_slots(batch), cus);
+  *grid = std::min(slots, cus);
   if (const char* env = std::getenv("FUSED_HOAD_BWD_BLOCKS")) {
     const long cap = std::atol(env);
     if (cap > 0) *grid = static_cast<int>(std::min<long>(*grid, cap));
@@ -1114,12 +1151,14 @@ extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* pa
   return check_launch("forward_kernel");
 }
 
-// Workspace: `slots` partial rows, then one z stash per (workgroup, wave); the grid never
-// exceeds `slots`, so both are sized by it.
 extern "C" size_t fhoad_backward_workspace_size(int64_t batch) {
   if (batch <= 0) return 0;
-  const size_t slots = static_cast<size_t>(backward_slots(batch));
-  return slots * (kRowStride * sizeof(float) + kBwdWaves * kStashF4PerWave * sizeof(f4));
+  return workspace_bytes_for(backward_slots(batch));
+}
+
+extern "C" size_t fhoad_poisson_adam_step_workspace_size(int64_t batch, int64_t boundary_count) {
+  if (batch <= 0 || boundary_count < 0) return 0;
+  return workspace_bytes_for(slots_for_tiles(backward_tiles(batch) + backward_tiles(boundary_count)));
 }
 
 extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const float* parameters,
@@ -1147,9 +1186,9 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
     return fail(FHOAD_ERROR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes,
                 needed);
   }
-  int grid = 0;
-  if (int st = backward_grid(batch, &grid)) return st;
   const int slots = backward_slots(batch);
+  int grid = 0;
+  if (int st = backward_grid(slots, &grid)) return st;
   float* partials = static_cast<float*>(workspace);
   f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
   hipLaunchKernelGGL(backward_kernel<false>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
@@ -1162,40 +1201,51 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
 }
 
 extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* source,
+                                       int64_t batch, const float* boundary,
+                                       int64_t boundary_count, double boundary_weight,
                                        float* parameters, float* exp_avg, float* exp_avg_sq,
                                        float* step, float* loss, float* grad_parameters,
                                        float* grad_coordinates, void* workspace,
-                                       size_t workspace_bytes, int64_t batch, double lr,
-                                       double beta1, double beta2, double eps,
-                                       double weight_decay, void* stream) {
+                                       size_t workspace_bytes, double lr, double beta1,
+                                       double beta2, double eps, double weight_decay,
+                                       void* stream) {
   if (batch <= 0) return fail(FHOAD_ERROR_INVALID_VALUE, "batch must be positive");
-  if (!coordinates || !source || !parameters || !exp_avg || !exp_avg_sq || !step || !loss) {
+  if (boundary_count < 0) return fail(FHOAD_ERROR_INVALID_VALUE, "boundary_count must be non-negative");
+  if (!coordinates || !source || !parameters || !exp_avg || !exp_avg_sq || !step || !loss ||
+      (boundary_count > 0 && !boundary)) {
     return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
   }
   if (!(lr >= 0.0) || !(eps >= 0.0) || !(beta1 >= 0.0 && beta1 < 1.0) ||
-      !(beta2 >= 0.0 && beta2 < 1.0) || !(weight_decay >= 0.0)) {
+      !(beta2 >= 0.0 && beta2 < 1.0) || !(weight_decay >= 0.0) || !(boundary_weight >= 0.0)) {
     return fail(FHOAD_ERROR_INVALID_VALUE,
-                "Adam needs lr >= 0, eps >= 0, 0 <= betas < 1 and weight_decay >= 0");
+                "Adam needs lr >= 0, eps >= 0, 0 <= betas < 1, weight_decay >= 0 and "
+                "boundary_weight >= 0");
   }
-  const size_t needed = fhoad_backward_workspace_size(batch);
+  const size_t needed = fhoad_poisson_adam_step_workspace_size(batch, boundary_count);
   if (!workspace || workspace_bytes < needed) {
     return fail(FHOAD_ERROR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes,
                 needed);
   }
+  const int64_t interior_tiles = backward_tiles(batch);
+  const int64_t tiles = interior_tiles + backward_tiles(boundary_count);
+  const int slots = slots_for_tiles(tiles);
   int grid = 0;
-  if (int st = backward_grid(batch, &grid)) return st;
+  if (int st = backward_grid(slots, &grid)) return st;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
-  const int slots = backward_slots(batch);
   const float inv_batch = 1.0f / static_cast<float>(batch);
+  const float weight = static_cast<float>(boundary_weight);
+  const float boundary_scale = boundary_count > 0 ? weight / static_cast<float>(boundary_count) : 0.0f;
+  const float inv_boundary = boundary_count > 0 ? 1.0f / static_cast<float>(boundary_count) : 0.0f;
   float* partials = static_cast<float*>(workspace);
   f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
+  const LossSeed seed{source, boundary, interior_tiles, boundary_count, inv_batch, boundary_scale, step};
   hipLaunchKernelGGL(backward_kernel<true>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
                      coordinates, parameters, nullptr, nullptr, grad_coordinates, partials, stash,
-                     batch, backward_tiles(batch), slots, LossSeed{source, inv_batch, step});
+                     batch, tiles, slots, seed);
   if (int st = check_launch("backward_kernel")) return st;
-  AdamArgs args{parameters, exp_avg, exp_avg_sq, step, loss, grad_parameters,
-                lr, beta1, beta2, eps, weight_decay, inv_batch};
-  hipLaunchKernelGGL(reduce_adam_kernel, dim3((kLossColumn + 1 + 63) / 64),
+  const AdamArgs args{parameters, exp_avg, exp_avg_sq, step, loss, grad_parameters,
+                      lr, beta1, beta2, eps, weight_decay, inv_batch, inv_boundary, weight};
+  hipLaunchKernelGGL(reduce_adam_kernel, dim3((kLossColumn + 2 + 63) / 64),
                      dim3(kReduceGroups * 64), 0, hs, partials, slots, args);
   return check_launch("reduce_adam_kernel");
 }

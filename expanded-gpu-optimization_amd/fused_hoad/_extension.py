@@ -84,9 +84,13 @@ def poisson_adam_step(
     weight_decay: float,
     grad_parameters: Tensor | None = None,
     grad_coordinates: Tensor | None = None,
+    boundary: Tensor | None = None,
+    boundary_weight: float = 100.0,
 ) -> Tensor:
-    """One fused Poisson-loss + Adam step (two gfx950 kernels); updates ``parameters``,
-    ``exp_avg``, ``exp_avg_sq`` and ``step`` in place and returns the loss at entry."""
+    """One fused Poisson PINN + Adam step (two gfx950 kernels); updates ``parameters``,
+    ``exp_avg``, ``exp_avg_sq`` and ``step`` in place and returns the loss at entry:
+    ``mean((Lap u - f)^2)`` over ``coordinates``, plus ``boundary_weight * mean(u^2)`` over
+    ``boundary`` when given."""
     return load_extension().poisson_adam_step(
         coordinates,
         source,
@@ -101,4 +105,6 @@ def poisson_adam_step(
         float(weight_decay),
         grad_parameters,
         grad_coordinates,
+        boundary,
+        float(boundary_weight),
     )

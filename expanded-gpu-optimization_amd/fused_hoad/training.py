@@ -108,10 +108,13 @@ class FusedPoissonAdam:
         (lap - source).pow(2).mean().backward()
         optimizer.step()
 
-    and returns the loss (a 0-dim device tensor, the loss before the update). The gradient
-    kernel re-runs the forward jet, so no separate forward launch is needed; it forms the
-    residual and its adjoint seed in registers. The reduction kernel sums the weight gradient
-    in a fixed order and applies Adam to each element in the same thread. Results are bitwise
+    or, given ``boundary`` points, the PINN step of
+    /root/reference/benchmarks/train_poisson.py:30-45 with the loss of ``poisson_loss_fn``,
+    ``mean((lap - source)^2) + boundary_weight * mean(model(boundary)^2)``. It returns the loss
+    (a 0-dim device tensor, the loss before the update). The gradient kernel re-runs the forward
+    jet, so no separate forward launch is needed; it forms the residual (or the boundary value)
+    and its adjoint seed in registers. The reduction kernel sums the weight gradient in a fixed
+    order and applies Adam to each element in the same thread. Results are bitwise
     reproducible.
 
     The model's parameters are moved into one packed buffer (``self.parameters``, the kernel
@@ -120,8 +123,9 @@ class FusedPoissonAdam:
     device (``step_count``), so a step can be captured in a HIP graph (``graphed``).
     ``keep_grads`` leaves the summed gradient in ``self.grad`` and, as views of it, in every
     parameter's ``.grad``; with ``coordinates.requires_grad`` the coordinate gradient goes to
-    ``self.grad_coordinates``. The coordinates and the source are read in place on every step:
-    to train on new points, copy them into ``self.coordinates`` / ``self.source``.
+    ``self.grad_coordinates``. The coordinates, the source and the boundary points are read in
+    place on every step: to train on new points, copy them into ``self.coordinates``,
+    ``self.source`` and ``self.boundary``.
     """
 
     def __init__(
@@ -130,6 +134,8 @@ class FusedPoissonAdam:
         coordinates: Tensor,
         source: Tensor | None = None,
         *,
+        boundary: Tensor | None = None,
+        boundary_weight: float = 100.0,
         lr: float = 1e-3,
         betas: tuple[float, float] = (0.9, 0.999),
         eps: float = 1e-8,
@@ -138,8 +144,8 @@ class FusedPoissonAdam:
     ) -> None:
         from fused_hoad.problems.poisson import manufactured_source
 
-        if not lr >= 0.0 or not eps >= 0.0 or not weight_decay >= 0.0:
-            raise ValueError("lr, eps and weight_decay must be non-negative")
+        if not lr >= 0.0 or not eps >= 0.0 or not weight_decay >= 0.0 or not boundary_weight >= 0.0:
+            raise ValueError("lr, eps, weight_decay and boundary_weight must be non-negative")
         if not (0.0 <= betas[0] < 1.0 and 0.0 <= betas[1] < 1.0):
             raise ValueError("betas must lie in [0, 1)")
         if coordinates.ndim != 2 or coordinates.shape[1] != 2 or coordinates.shape[0] == 0:
@@ -155,6 +161,10 @@ class FusedPoissonAdam:
         if source.numel() != coordinates.shape[0]:
             raise ValueError("source must hold one value per point")
         self.source = source.detach().reshape(-1).contiguous()
+        if boundary is not None and (boundary.ndim != 2 or boundary.shape[1] != 2):
+            raise ValueError("boundary must have shape [count, 2]")
+        self.boundary = None if boundary is None else boundary.detach().contiguous()
+        self.boundary_weight = boundary_weight
         self.exp_avg = torch.zeros_like(self.parameters)
         self.exp_avg_sq = torch.zeros_like(self.parameters)
         self.step_count = torch.zeros(1, dtype=torch.float32, device=self.parameters.device)
@@ -185,6 +195,8 @@ class FusedPoissonAdam:
             weight_decay=self.weight_decay,
             grad_parameters=self.grad,
             grad_coordinates=self.grad_coordinates,
+            boundary=self.boundary,
+            boundary_weight=self.boundary_weight,
         )
 
     def step(self) -> Tensor:

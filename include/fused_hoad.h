@@ -88,35 +88,50 @@ int fhoad_forward_laplacian_backward(const float* coordinates, const float* para
                                      int version, void* stream);
 
 /*
+ * Bytes of device workspace fhoad_poisson_adam_step needs for `batch` interior and
+ * `boundary_count` boundary points. 0 for batch <= 0 or boundary_count < 0.
+ */
+size_t fhoad_poisson_adam_step_workspace_size(int64_t batch, int64_t boundary_count);
+
+/*
  * One fused training step of the Poisson PINN loss with Adam:
- *   loss = mean_b (laplacian(x_b) - source[b])^2, then one torch.optim.Adam update
- *   (amsgrad = False, maximize = False) of `parameters` in place.
- * Two kernels on `stream`: the gradient kernel re-runs the forward jet, forms the residual and
- * its adjoint seed (grad_u = 0, grad_lap = (1 / B) 2 r) in registers and walks the adjoint
- * back; the reduction kernel sums the weight gradient in the backward's fixed order and
- * applies Adam to each element in the same thread.
+ *   loss = mean_b (laplacian(x_b) - source[b])^2
+ *          + boundary_weight * mean_k u(boundary_k)^2      (term absent when boundary_count == 0)
+ * then one torch.optim.Adam update (amsgrad = False, maximize = False) of `parameters` in place.
+ * Two kernels on `stream`:
+ *   - the gradient kernel re-runs the forward jet, forms the residual (interior points) or u
+ *     (boundary points) and the adjoint seed autograd would form for the loss in registers, and
+ *     walks the adjoint back;
+ *   - the reduction kernel sums the weight gradient in the backward's fixed order and applies
+ *     Adam to each element in the same thread.
+ * Arguments:
+ *   coordinates, source: [batch][2] interior points and f[batch].
+ *   boundary: [boundary_count][2] boundary points (NULL allowed when boundary_count == 0).
  *   parameters, exp_avg, exp_avg_sq: [12737] each, updated in place (Adam's first and second
  *     moments share the packed parameter layout).
  *   step: one float, the number of Adam steps taken so far; incremented on the device, so the
  *     call can be captured in a HIP graph and replayed.
  *   loss: one float, written with the loss of the parameters on entry.
  *   grad_parameters: optional [12737] copy of the summed gradient (NULL: not written).
- *   grad_coordinates: optional [batch][2] dLoss/dcoordinates (NULL: not written).
- *   workspace: fhoad_backward_workspace_size(batch) bytes.
+ *   grad_coordinates: optional [batch][2] dLoss/d(interior coordinates) (NULL: not written).
+ *   workspace: fhoad_poisson_adam_step_workspace_size(batch, boundary_count) bytes.
  * Results are bitwise reproducible and do not depend on the grid size. batch must be > 0
- * (the loss of an empty batch is undefined).
+ * (the loss of an empty interior set is undefined).
  *
- * Replaces, as one call, the step of /root/reference/benchmarks/benchmark_training.py:41-60:
- * fused_forward_laplacian_cuda (csrc/fused_residual.cu:587-643), the loss
- * (lap - source).pow(2).mean() and its autograd backward (benchmark_training.py:46-48),
- * fused_forward_laplacian_backward_cuda (csrc/fused_backward.cu:859-934), the
- * differentiable pack (src/fused_hoad/parameters.py:77-78) and torch.optim.Adam.step
- * (benchmark_training.py:41).
+ * Replaces, as one call, the Python training step of
+ * /root/reference/benchmarks/train_poisson.py:30-45 and
+ * /root/reference/benchmarks/benchmark_training.py:41-60:
+ *   - fused_forward_laplacian_cuda (csrc/fused_residual.cu:587-643);
+ *   - the loss of src/fused_hoad/training.py:66-88 and its autograd backward;
+ *   - fused_forward_laplacian_backward_cuda (csrc/fused_backward.cu:859-934);
+ *   - the differentiable pack (src/fused_hoad/parameters.py:77-78);
+ *   - torch.optim.Adam.step.
  */
-int fhoad_poisson_adam_step(const float* coordinates, const float* source, float* parameters,
-                            float* exp_avg, float* exp_avg_sq, float* step, float* loss,
-                            float* grad_parameters, float* grad_coordinates, void* workspace,
-                            size_t workspace_bytes, int64_t batch, double lr, double beta1,
+int fhoad_poisson_adam_step(const float* coordinates, const float* source, int64_t batch,
+                            const float* boundary, int64_t boundary_count, double boundary_weight,
+                            float* parameters, float* exp_avg, float* exp_avg_sq, float* step,
+                            float* loss, float* grad_parameters, float* grad_coordinates,
+                            void* workspace, size_t workspace_bytes, double lr, double beta1,
                             double beta2, double eps, double weight_decay, void* stream);
 
 #ifdef __cplusplus

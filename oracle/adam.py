@@ -12,18 +12,22 @@ What it restates:
   /root/reference/benchmarks/benchmark_training.py:41 (``torch.optim.Adam(lr=1e-3)``):
   ``g += wd p; m = b1 m + (1 - b1) g; v = b2 v + (1 - b2) g^2;
   p -= lr (m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps)``.
-* ``poisson_adam_step``: the step of /root/reference/benchmarks/benchmark_training.py:46-60:
-  ``loss = mean((lap - f)^2)`` from the forward jet (``jet.forward``), backward with the
-  upstream gradients autograd forms for that loss (grad_u = 0, grad_lap = 2 (lap - f) / B,
-  fed to ``jet.backward``), then ``adam_update`` of the packed buffer (Adam is elementwise,
-  so running it on the packed 12,737 floats equals running it per parameter tensor).
+* ``poisson_adam_step``: the step of /root/reference/benchmarks/benchmark_training.py:46-60
+  and, with boundary points, of /root/reference/benchmarks/train_poisson.py:30-45 (loss of
+  src/fused_hoad/training.py:66-88):
+  ``loss = mean((lap - f)^2) + w mean(u_b^2)`` from the forward jet (``jet.forward``),
+  backward with the upstream gradients autograd forms for that loss (interior:
+  grad_u = 0, grad_lap = 2 (lap - f) / B; boundary: grad_u = 2 w u_b / B_b, grad_lap = 0, fed
+  to ``jet.backward``), then ``adam_update`` of the packed buffer (Adam is elementwise, so
+  running it on the packed 12,737 floats equals running it per parameter tensor).
 
 How it is pinned (tests/test_adam_oracle.py): against torch.optim.Adam itself on the CPU in
 float64 (the library routine the reference calls) over several steps with and without
 weight decay; against the closed form of the first step from zero state
 (``p1 = p0 - lr g / (|g| + eps)``); against planted mistakes (a dropped bias correction, a
 swapped beta) that those checks must reject; and, for the loss seed, against torch autograd
-of ``(lap - f).pow(2).mean()``.
+of ``(lap - f).pow(2).mean()``; the whole step, boundary term included, against a float64
+torch training step with autograd and torch.optim.Adam.
 """
 
 from __future__ import annotations
@@ -56,17 +60,26 @@ def poisson_seed(lap, source):
     return float(np.mean(r * r)), 2.0 * r / r.size
 
 
-def poisson_adam_step(params, coordinates, source, exp_avg, exp_avg_sq, step, **adam):
+def poisson_adam_step(params, coordinates, source, exp_avg, exp_avg_sq, step, *, boundary=None,
+                      boundary_weight=100.0, **adam):
     """One fused step: loss and gradients at ``params``, then Adam.
 
-    ``step`` is the step count after this update. Returns a dict with ``loss``,
-    ``grad_parameters``, ``grad_coordinates``, ``params``, ``exp_avg``, ``exp_avg_sq``.
+    ``step`` is the step count after this update. With ``boundary`` points the loss gains
+    ``boundary_weight * mean(u(boundary)^2)``. Returns a dict with ``loss``,
+    ``grad_parameters``, ``grad_coordinates`` (interior points), ``params``, ``exp_avg``,
+    ``exp_avg_sq``.
     """
     p = np.asarray(params, dtype=np.float64)
     x = np.asarray(coordinates, dtype=np.float64)
     _, lap = jet.forward(p, x)
     loss, grad_lap = poisson_seed(lap, source)
     grad_p, grad_x = jet.backward(p, x, np.zeros_like(grad_lap), grad_lap)
+    if boundary is not None and len(boundary):
+        xb = np.asarray(boundary, dtype=np.float64)
+        ub, _ = jet.forward(p, xb)
+        loss += boundary_weight * float(np.mean(ub * ub))
+        grad_pb, _ = jet.backward(p, xb, 2.0 * boundary_weight * ub / ub.size, np.zeros_like(ub))
+        grad_p = grad_p + grad_pb
     new_p, m, v = adam_update(p, grad_p, exp_avg, exp_avg_sq, step, **adam)
     return {
         "loss": loss,

@@ -132,3 +132,35 @@ def test_poisson_adam_step_matches_a_torch_training_step() -> None:
     assert out["loss"] == pytest.approx(loss.item(), rel=1e-12)
     np.testing.assert_allclose(out["grad_parameters"], grad, rtol=1e-9, atol=1e-12 * np.abs(grad).max())
     np.testing.assert_allclose(out["params"], leaf.detach().numpy(), rtol=1e-12, atol=1e-14)
+
+
+def test_pinn_step_with_boundary_matches_a_torch_training_step() -> None:
+    """The oracle's PINN step (boundary term included) against the reference's loss of
+    training.py:66-88 in float64 on the CPU: forward Laplacian on the interior, a plain MLP
+    forward on the boundary, autograd, torch.optim.Adam."""
+    from fused_hoad.problems.poisson import manufactured_source
+    from fused_hoad.training import boundary_points
+
+    flat = torch_ref.pack(torch_ref.reference_model(1)).double()
+    gen = torch.Generator().manual_seed(5)
+    x = torch.rand(200, 2, generator=gen, dtype=torch.float64) * 2 - 1
+    xb = boundary_points(70, device="cpu", dtype=torch.float64, generator=gen)
+    f = manufactured_source(x)
+
+    leaf = torch.nn.Parameter(flat.clone())
+    opt = torch.optim.Adam([leaf], lr=1e-3, foreach=False)
+    _, lap = torch_ref.forward_laplacian(leaf, x)
+    loss = (lap - f).pow(2).mean() + 100.0 * torch_ref._mlp(leaf, xb).pow(2).mean()
+    loss.backward()
+    grad = leaf.grad.detach().numpy().copy()
+    opt.step()
+
+    zeros = np.zeros(jet.PARAMETER_COUNT)
+    out = adam.poisson_adam_step(flat.numpy(), x.numpy(), f.numpy(), zeros, zeros, 1,
+                                 boundary=xb.numpy(), boundary_weight=100.0, lr=1e-3)
+    assert out["loss"] == pytest.approx(loss.item(), rel=1e-12)
+    np.testing.assert_allclose(out["grad_parameters"], grad, rtol=1e-9, atol=1e-12 * np.abs(grad).max())
+    np.testing.assert_allclose(out["params"], leaf.detach().numpy(), rtol=1e-12, atol=1e-14)
+    # the boundary term matters: without it the gradient differs
+    plain = adam.poisson_adam_step(flat.numpy(), x.numpy(), f.numpy(), zeros, zeros, 1, lr=1e-3)
+    assert not np.allclose(plain["grad_parameters"], grad, rtol=1e-3, atol=0)

@@ -36,7 +36,11 @@ def _lib() -> ctypes.CDLL:
     lib.fhoad_forward_laplacian_backward.argtypes = [vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, i64, ci, vp]
     d = ctypes.c_double
     lib.fhoad_poisson_adam_step.restype = ci
-    lib.fhoad_poisson_adam_step.argtypes = [vp] * 10 + [ctypes.c_size_t, i64, d, d, d, d, d, vp]
+    lib.fhoad_poisson_adam_step.argtypes = (
+        [vp, vp, i64, vp, i64, d] + [vp] * 8 + [ctypes.c_size_t, d, d, d, d, d, vp]
+    )
+    lib.fhoad_poisson_adam_step_workspace_size.restype = ctypes.c_size_t
+    lib.fhoad_poisson_adam_step_workspace_size.argtypes = [i64, i64]
     return lib
 
 
@@ -54,6 +58,7 @@ def test_header_declares_the_entry_points() -> None:
         "fhoad_last_error",
         "fhoad_parameter_count",
         "fhoad_poisson_adam_step",
+        "fhoad_poisson_adam_step_workspace_size",
         "fhoad_status_string",
     ]
 
@@ -81,6 +86,12 @@ def test_workspace_size_is_one_partial_row_and_stash_per_slot() -> None:
     assert lib.fhoad_backward_workspace_size(65) == 2 * per_slot
     assert lib.fhoad_backward_workspace_size(65536) == 256 * per_slot
     assert lib.fhoad_backward_workspace_size(1 << 20) == 256 * per_slot
+    # the fused step's slots cover the interior tiles and the boundary tiles
+    assert lib.fhoad_poisson_adam_step_workspace_size(0, 5) == 0
+    assert lib.fhoad_poisson_adam_step_workspace_size(64, 0) == per_slot
+    assert lib.fhoad_poisson_adam_step_workspace_size(65, 1) == 3 * per_slot
+    assert lib.fhoad_poisson_adam_step_workspace_size(16384, 1024) == 256 * per_slot
+    assert lib.fhoad_poisson_adam_step_workspace_size(1000, 200) == (16 + 4) * per_slot
 
 
 def test_argument_errors_are_reported_before_any_device_work() -> None:
@@ -94,16 +105,26 @@ def test_argument_errors_are_reported_before_any_device_work() -> None:
     assert b"backward version must be 1 to 6" in lib.fhoad_last_error()
     assert lib.fhoad_forward_laplacian_backward(None, None, None, None, None, None, None, 0, -3, 6, None) == 2
     step = lib.fhoad_poisson_adam_step
-    assert step(*[None] * 10, 0, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0, None) == 2
+    adam = (1e-3, 0.9, 0.999, 1e-8, 0.0)
+
+    def call(ptr, batch, boundary, count, weight, ws_bytes, *hyper):
+        # coordinates, source, batch, boundary, count, weight, 7 state/output pointers, ws
+        return step(ptr, ptr, batch, boundary, count, weight, *[ptr] * 5, None, None, ptr,
+                    ws_bytes, *hyper, None)
+
+    fake = ctypes.c_void_p(256)  # non-null, never dereferenced: the checks fail first
+    assert call(None, 0, None, 0, 100.0, 0, *adam) == 2
     assert b"batch must be positive" in lib.fhoad_last_error()
-    assert step(*[None] * 10, 0, 16, 1e-3, 0.9, 0.999, 1e-8, 0.0, None) == 2
+    assert call(None, 16, None, 0, 100.0, 0, *adam) == 2
     assert b"null device pointer" in lib.fhoad_last_error()
-    # Dummy non-null addresses: the argument checks fail before anything is dereferenced.
-    fake = [ctypes.c_void_p(256)] * 7 + [None, None, ctypes.c_void_p(256)]
-    assert step(*fake, 1 << 30, 16, 1e-3, 1.0, 0.999, 1e-8, 0.0, None) == 2
+    assert call(fake, 16, None, 5, 100.0, 1 << 30, *adam) == 2  # boundary points missing
+    assert call(fake, 16, None, -1, 100.0, 1 << 30, *adam) == 2
+    assert call(fake, 16, None, 0, 100.0, 1 << 30, 1e-3, 1.0, 0.999, 1e-8, 0.0) == 2
     assert b"betas" in lib.fhoad_last_error()
-    assert step(*fake, 1 << 30, 16, -1e-3, 0.9, 0.999, 1e-8, 0.0, None) == 2
-    assert step(*fake, 10, 16, 1e-3, 0.9, 0.999, 1e-8, 0.0, None) == 4
+    assert call(fake, 16, None, 0, 100.0, 1 << 30, -1e-3, 0.9, 0.999, 1e-8, 0.0) == 2
+    assert call(fake, 16, None, 0, -1.0, 1 << 30, *adam) == 2
+    assert call(fake, 16, None, 0, 100.0, 10, *adam) == 4
+    assert call(fake, 16, fake, 300, 100.0, lib.fhoad_poisson_adam_step_workspace_size(16, 200), *adam) == 4
 
 
 def test_torch_extension_reports_contract_errors_on_cpu() -> None:
@@ -165,13 +186,15 @@ def test_raw_fused_step_matches_the_torch_extension() -> None:
     from gpu_helpers import announce, coordinates, packed, require_gpu_extension
 
     require_gpu_extension()
-    announce("C ABI fhoad_poisson_adam_step via ctypes vs fused_hoad._C, batch=3000")
+    announce("C ABI fhoad_poisson_adam_step via ctypes vs fused_hoad._C, batch=3000 + 300 boundary")
     from fused_hoad import _C, manufactured_source
+    from fused_hoad.training import boundary_points
 
     lib = _lib()
-    batch = 3000
+    batch, nb = 3000, 300
     x = coordinates(batch, seed=13)
     f = manufactured_source(x).reshape(-1).contiguous()
+    xb = boundary_points(nb, device="cpu", generator=torch.Generator().manual_seed(13)).cuda()
     stream = torch.cuda.current_stream().cuda_stream
 
     def state():
@@ -182,20 +205,21 @@ def test_raw_fused_step_matches_the_torch_extension() -> None:
     loss = torch.empty((), device="cuda")
     gp = torch.empty(12737, device="cuda")
     gx = torch.empty(batch, 2, device="cuda")
-    ws_bytes = lib.fhoad_backward_workspace_size(batch)
+    ws_bytes = lib.fhoad_poisson_adam_step_workspace_size(batch, nb)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
     for _ in range(2):
         status = lib.fhoad_poisson_adam_step(
-            x.data_ptr(), f.data_ptr(), p.data_ptr(), m.data_ptr(), v.data_ptr(), t.data_ptr(),
-            loss.data_ptr(), gp.data_ptr(), gx.data_ptr(), ws.data_ptr(), ws_bytes, batch,
-            1e-3, 0.9, 0.999, 1e-8, 0.0, stream)
+            x.data_ptr(), f.data_ptr(), batch, xb.data_ptr(), nb, 100.0, p.data_ptr(),
+            m.data_ptr(), v.data_ptr(), t.data_ptr(), loss.data_ptr(), gp.data_ptr(),
+            gx.data_ptr(), ws.data_ptr(), ws_bytes, 1e-3, 0.9, 0.999, 1e-8, 0.0, stream)
         assert status == 0, lib.fhoad_last_error()
 
     ep, em, ev, et = state()
     egp = torch.empty_like(gp)
     egx = torch.empty_like(gx)
     for _ in range(2):
-        eloss = _C.poisson_adam_step(x, f, ep, em, ev, et, 1e-3, 0.9, 0.999, 1e-8, 0.0, egp, egx)
+        eloss = _C.poisson_adam_step(x, f, ep, em, ev, et, 1e-3, 0.9, 0.999, 1e-8, 0.0, egp, egx,
+                                     xb, 100.0)
     torch.cuda.synchronize()
     for a, b in ((p, ep), (m, em), (v, ev), (t, et), (loss, eloss), (gp, egp), (gx, egx)):
         assert torch.equal(a, b)

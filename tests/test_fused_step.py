@@ -256,3 +256,84 @@ def test_argument_errors() -> None:
         _C.poisson_adam_step(x[:0], f[:0], p, p.clone(), p.clone(), step, 1e-3, 0.9, 0.999, 1e-8, 0.0)
     with pytest.raises(RuntimeError, match="betas"):
         _C.poisson_adam_step(x, f, p, p.clone(), p.clone(), step, 1e-3, 1.5, 0.999, 1e-8, 0.0)
+
+
+def _boundary(count: int, seed: int):
+    from fused_hoad.training import boundary_points
+
+    return boundary_points(count, device="cpu", generator=torch.Generator().manual_seed(seed)).cuda()
+
+
+@pytest.mark.parametrize("batch,nb", [(1000, 100), (100, 1), (100, 63), (64, 64), (100, 65), (20000, 1024)])
+def test_pinn_step_with_boundary_matches_the_oracle(batch: int, nb: int) -> None:
+    announce(f"fused PINN+Adam step (boundary term) vs float64 oracle, batch={batch}, boundary={nb}")
+    from oracle import adam
+    from fused_hoad.training import FusedPoissonAdam
+
+    model = _model(2)
+    x = coordinates(batch, seed=14)
+    xb = _boundary(nb, 14)
+    trainer = FusedPoissonAdam(model, x, boundary=xb, boundary_weight=100.0, lr=1e-3)
+    p0 = to_numpy64(trainer.parameters)
+    loss = trainer.step()
+    torch.cuda.synchronize()
+    want = adam.poisson_adam_step(p0, to_numpy64(x), to_numpy64(trainer.source), np.zeros_like(p0),
+                                  np.zeros_like(p0), 1, boundary=to_numpy64(xb), boundary_weight=100.0)
+    assert float(loss) == pytest.approx(want["loss"], rel=2e-5)
+    got_grad = to_numpy64(trainer.grad)
+    for name, start, end in _blocks():
+        assert_scaled_close(got_grad[start:end], want["grad_parameters"][start:end], 1e-4, name)
+    p1, _, _ = adam.adam_update(p0, got_grad, np.zeros_like(p0), np.zeros_like(p0), 1)
+    np.testing.assert_allclose(to_numpy64(trainer.parameters), p1, rtol=0, atol=2e-7 * np.abs(p0).max() + 1e-9)
+
+
+def test_pinn_step_matches_the_reference_pinn_loss_path() -> None:
+    """20 PINN steps against the reference's poisson_loss_fn (training.py:66-88) on the fused
+    backend with torch.optim.Adam, as train_poisson.py runs it: loss curve within rtol 1e-3."""
+    announce("FusedPoissonAdam(boundary) vs poisson_loss_fn(fused_cuda) + torch Adam, 20 steps")
+    from fused_hoad import get_backend
+    from fused_hoad.training import FusedPoissonAdam, poisson_loss_fn
+
+    x = coordinates(16384, seed=15)
+    xb = _boundary(1024, 15)
+    ref_model = _model()
+    optimizer = torch.optim.Adam(ref_model.parameters(), lr=1e-3)
+    loss_fn = poisson_loss_fn(get_backend("fused_cuda"), ref_model, x, xb)
+    ref_losses = []
+    for _ in range(20):
+        optimizer.zero_grad(set_to_none=True)
+        loss = loss_fn()
+        loss.backward()
+        optimizer.step()
+        ref_losses.append(loss.item())
+
+    model = _model()
+    trainer = FusedPoissonAdam(model, x, boundary=xb, boundary_weight=100.0, lr=1e-3)
+    losses = [trainer.step().item() for _ in range(20)]
+    np.testing.assert_allclose(losses, ref_losses, rtol=1e-3)
+    for a, b in zip(model.parameters(), ref_model.parameters()):
+        torch.testing.assert_close(a, b, rtol=0, atol=2e-5)
+
+
+def test_pinn_step_is_bitwise_deterministic_and_grid_independent() -> None:
+    announce("FusedPoissonAdam(boundary) determinism: 2 runs + FUSED_HOAD_BWD_BLOCKS=5")
+    from fused_hoad.training import FusedPoissonAdam
+
+    x = coordinates(16384, seed=16)
+    xb = _boundary(1024, 16)
+
+    def run():
+        trainer = FusedPoissonAdam(_model(), x, boundary=xb)
+        losses = torch.stack([trainer.step() for _ in range(3)])
+        torch.cuda.synchronize()
+        return losses, trainer.parameters.clone(), trainer.grad.clone()
+
+    first = run()
+    second = run()
+    os.environ["FUSED_HOAD_BWD_BLOCKS"] = "5"
+    try:
+        capped = run()
+    finally:
+        del os.environ["FUSED_HOAD_BWD_BLOCKS"]
+    for a, b, c in zip(first, second, capped):
+        assert torch.equal(a, b) and torch.equal(a, c)

@@ -1,0 +1,34 @@
+"""The end-to-end PINN driver (fused_hoad.train_poisson, the behaviour of the reference's
+benchmarks/train_poisson.py) runs every backend, eager and HIP-graph, on a short schedule."""
+
+from __future__ import annotations
+
+import pytest
+
+from gpu_helpers import announce, require_gpu_extension
+
+pytestmark = pytest.mark.gpu
+
+
+def test_driver_trains_every_mode(capsys) -> None:
+    require_gpu_extension()
+    announce("train_poisson driver: fused_step + fused_cuda, eager and graph, 40 steps")
+    from fused_hoad import train_poisson
+
+    train_poisson.main(["--backends", "fused_step", "fused_cuda", "--steps", "40", "--eval-every", "20",
+                        "--interior", "2048", "--boundary", "128", "--seeds", "0", "1", "--cuda-graph",
+                        "--target", "10.0"])
+    out = capsys.readouterr().out
+    rows = [line.split() for line in out.splitlines() if line.split()[:1] in (["fused_step"], ["fused_cuda"])]
+    assert len(rows) == 2 * 2 * 3  # backends x graph modes x (2 seeds + median)
+    for row in rows:
+        if row[2] != "med":
+            loss, rel_l2 = float(row[4]), float(row[5])
+            assert loss == loss and 0.0 < rel_l2 < 10.0
+            # target 10.0 is met at the first evaluation: 20 steps after the graph's warmup
+            # steps, which count as training (1 for fused_step, 3 for cuda_graph_step)
+            warmup = 0 if row[1] == "no" else (1 if row[0] == "fused_step" else 3)
+            assert row[7] != "never" and int(row[8]) == 20 + warmup
+    # the two eager runs of a seed agree closely (same loss, same Adam, fused kernels)
+    eager = {(r[0], r[2]): float(r[4]) for r in rows if r[1] == "no" and r[2] != "med"}
+    assert eager[("fused_step", "0")] == pytest.approx(eager[("fused_cuda", "0")], rel=1e-3)
