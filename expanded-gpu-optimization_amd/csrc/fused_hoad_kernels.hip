@@ -304,24 +304,35 @@ __device__ __forceinline__ void hidden_product_native(const f4* wa, const f4 (&h
 
 // Transposed product hb[ib][c] = sum_o W[o][16 ib + .] zb[o][c][.]: the adjoint of a hidden
 // layer's input. zb is in the same register layout as h; w points at this lane's column base.
+// The A operands of k-step n + 1 are read from LDS before the 16 MFMAs of k-step n are issued,
+// so the read latency hides behind MFMA work (one wave per SIMD has no other wave to switch to).
 __device__ __forceinline__ void hidden_product_t(const float* w, const f4 (&zb)[4][4],
                                                  f4 (&hb)[4][4]) {
+  float next[4];
 #pragma unroll
-  for (int ob = 0; ob < 4; ++ob) {
+  for (int ib = 0; ib < 4; ++ib) next[ib] = w[16 * ib];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float a[4];
+  for (int step = 0; step < 16; ++step) {
+    const int ob = step >> 2, j = step & 3;
+    float a[4];
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) a[ib] = w[1088 * ob + kWRow * j + 16 * ib];
+    for (int ib = 0; ib < 4; ++ib) a[ib] = next[ib];
+    if (step < 15) {
+      const int nob = (step + 1) >> 2, nj = (step + 1) & 3;
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
+      for (int ib = 0; ib < 4; ++ib) next[ib] = w[1088 * nob + kWRow * nj + 16 * ib];
+    }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const f4 cin = (ob | j) ? hb[ib][c] : f4{0.f, 0.f, 0.f, 0.f};
-          hb[ib][c] = mfma(a[ib], zb[ob][c][j], cin);
-        }
+    for (int ib = 0; ib < 4; ++ib) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f4 cin = (ob | j) ? hb[ib][c] : f4{0.f, 0.f, 0.f, 0.f};
+        hb[ib][c] = mfma(a[ib], zb[ob][c][j], cin);
       }
     }
+    // Schedule: the next step's two DS reads, then this step's 16 MFMAs.
+    if (step < 15) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
   }
 }
 
@@ -710,7 +721,10 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   const int rows_off = lane_rows(m, g);
   const int cols_off = lane_cols(m, g);
   const int stage_lane_off = cols_off + 16 * w;
-  f4* my_stash = stash + static_cast<int64_t>(blockIdx.x * kBwdWaves + w) * kStashF4PerWave + lane;
+  // This lane's slot in its wave's stash, as an offset from the kernel argument (an opaque
+  // pointer would lose its global address space and become flat accesses, which also hold up
+  // every LDS wait).
+  const int64_t stash_off = static_cast<int64_t>(blockIdx.x * kBwdWaves + w) * kStashF4PerWave + lane;
 
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
     f4 dw[3][4];
@@ -749,7 +763,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       {
         f4 z1[4][4];
         hidden_layer(s_small, s_w + opaque(rows_off), 0, g, h, z1);
-        f4* stash_st = opaque(my_stash);
+        f4* stash_st = stash + opaque(stash_off);
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -824,7 +838,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 
       // ---- 4. hidden layer 2 (needs hidden layer 1's z back from the stash) ----
       keep_lds_reads_in_loop();  // the reload below must read memory, not forward the stores
-      const f4* stash_ld = opaque(my_stash);
+      const f4* stash_ld = stash + opaque(stash_off);
       f4 z1[4][4];
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
