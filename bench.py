@@ -10,6 +10,12 @@ the forward and seeds itself from the loss, one reduction kernel with the Adam u
 the reference's step through the drop-in API (fused forward + autograd loss + fused backward +
 torch.optim.Adam).
 
+Timing: each quantity is K calls run back to back between two synchronizes; `value` and the
+step times come from the host clock over those calls, and each kernel's average duration (the
+roofline's `avg_launch_ms`) from one HIP event pair on the launch stream around the same calls.
+A separate pass with an event pair per call gives the median and p90 in the log only (per-call
+event packets add their own time to each call).
+
 Correctness is checked before any timing: the fused forward against the package's PyTorch
 forward Laplacian (atol 1e-5 / rtol 1e-4) and the fused backward against the PyTorch
 recompute backward (1e-4 of each gradient block's scale); a mismatch aborts.
@@ -75,20 +81,40 @@ def _gpu_clock_mhz() -> float | None:
     return None
 
 
-def _events_timed(fn, iterations: int, torch):
-    """Run fn `iterations` times bracketed by synchronize; per-call HIP events on the current
-    stream (the stream the kernels are launched on). Returns (total_ms, per_call_ms list)."""
+def _timed(fn, iterations: int, torch):
+    """Run fn `iterations` times back to back, bracketed by synchronize, with one HIP event
+    pair on the current stream (the stream the kernels run on) around the whole region.
+    Returns (wall_ms, gpu_ms) totals. Nothing is recorded between calls, so the calls run as a
+    caller would run them."""
+    stream = torch.cuda.current_stream()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    begin.record(stream)
+    for _ in range(iterations):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - start) * 1e3, begin.elapsed_time(end)
+
+
+def _per_call_events(fn, iterations: int, torch) -> list[float]:
+    """Per-call HIP event pairs (ms), for the median and p90 in the log; the event packets
+    between calls add their own time, so these are not used for `value`."""
     stream = torch.cuda.current_stream()
     pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iterations)]
     torch.cuda.synchronize()
-    start = time.perf_counter()
     for begin, end in pairs:
         begin.record(stream)
         fn()
         end.record(stream)
     torch.cuda.synchronize()
-    total_ms = (time.perf_counter() - start) * 1e3
-    return total_ms, [b.elapsed_time(e) for b, e in pairs]
+    return [b.elapsed_time(e) for b, e in pairs]
+
+
+def _p90(samples: list[float]) -> float:
+    ordered = sorted(samples)
+    return ordered[min(len(ordered) - 1, int(0.9 * len(ordered)))]
 
 
 def _scaled_error(actual, expected) -> float:
@@ -152,13 +178,14 @@ def main() -> None:
 
     for _ in range(args.warmup):
         residual_step()
-    total_ms, per_call = _events_timed(residual_step, args.steps, torch)
+    total_ms, gpu_ms = _timed(residual_step, args.steps, torch)
     ms_per_step = total_ms / args.steps
-    fwd_kernel_ms = statistics.mean(per_call)
+    fwd_kernel_ms = gpu_ms / args.steps
     points_per_s = args.points / (ms_per_step / 1e3)
-    log(f"residual {args.points} pts: {ms_per_step * 1e3:.1f} us/step wall, "
-        f"{fwd_kernel_ms * 1e3:.1f} us/call (events, mean), median {statistics.median(per_call) * 1e3:.1f} us, "
-        f"{points_per_s / 1e6:.1f} M points/s")
+    per_call = _per_call_events(residual_step, args.steps, torch)
+    log(f"residual {args.points} pts: {ms_per_step * 1e3:.1f} us/step wall, {fwd_kernel_ms * 1e3:.1f} us/call "
+        f"(GPU events over the {args.steps} calls), {points_per_s / 1e6:.1f} M points/s; per-call events: "
+        f"median {statistics.median(per_call) * 1e3:.1f} us, p90 {_p90(per_call) * 1e3:.1f} us")
 
     # ---- backward call alone (backward kernel + fixed-order reduction) ----
     def backward_step():
@@ -166,11 +193,11 @@ def main() -> None:
 
     for _ in range(args.warmup):
         backward_step()
-    _, bwd_calls = _events_timed(backward_step, args.steps, torch)
-    bwd_ms = statistics.mean(bwd_calls)
+    _, bwd_gpu_ms = _timed(backward_step, args.steps, torch)
+    bwd_ms = bwd_gpu_ms / args.steps
 
     if args.kernels_only:
-        log(f"backward call {args.train_points} pts: {bwd_ms * 1e3:.1f} us (events, mean)")
+        log(f"backward call {args.train_points} pts: {bwd_ms * 1e3:.1f} us (GPU events over the calls)")
         return
 
     # ---- training step (a): the reference's step through the drop-in API ----
@@ -187,10 +214,9 @@ def main() -> None:
 
     for _ in range(args.warmup):
         autograd_step()
-    autograd_total_ms, autograd_calls = _events_timed(autograd_step, args.steps, torch)
+    autograd_total_ms, _ = _timed(autograd_step, args.steps, torch)
     autograd_ms = autograd_total_ms / args.steps
-    log(f"train step (autograd drop-in) {args.train_points} pts: {autograd_ms:.3f} ms wall/step, "
-        f"median {statistics.median(autograd_calls):.3f} ms (events)")
+    log(f"train step (autograd drop-in) {args.train_points} pts: {autograd_ms:.3f} ms wall/step")
 
     # ---- training step (b): the fused step, FusedPoissonAdam (2 kernels) ----
     torch.manual_seed(0)
@@ -215,21 +241,21 @@ def main() -> None:
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats(device)
     baseline_bytes = torch.cuda.memory_allocated(device)
-    train_total_ms, train_calls = _events_timed(trainer.step, args.steps, torch)
+    train_total_ms, train_gpu_ms = _timed(trainer.step, args.steps, torch)
     train_ms = train_total_ms / args.steps
     peak_mib = (torch.cuda.max_memory_allocated(device) - baseline_bytes) / 2**20
+    train_calls = _per_call_events(trainer.step, args.steps, torch)
     log(f"train step (fused) {args.train_points} pts: {train_ms:.3f} ms wall/step, "
-        f"median {statistics.median(train_calls):.3f} ms (events); backward call {bwd_ms * 1e3:.1f} us; "
-        f"peak {peak_mib:.1f} MiB above baseline")
+        f"{train_gpu_ms / args.steps:.3f} ms GPU/step; per-call events median {statistics.median(train_calls):.3f} ms, "
+        f"p90 {_p90(train_calls):.3f} ms; backward call {bwd_ms * 1e3:.1f} us; peak {peak_mib:.1f} MiB above baseline")
 
     # ---- training step (c): the fused step replayed from a HIP graph ----
     replay = trainer.graphed(warmup=1)
     for _ in range(args.warmup):
         replay()
-    graph_total_ms, graph_calls = _events_timed(replay, args.steps, torch)
+    graph_total_ms, _ = _timed(replay, args.steps, torch)
     graph_ms = graph_total_ms / args.steps
-    log(f"train step (fused, HIP graph) {args.train_points} pts: {graph_ms:.3f} ms wall/step, "
-        f"median {statistics.median(graph_calls):.3f} ms (events)")
+    log(f"train step (fused, HIP graph) {args.train_points} pts: {graph_ms:.3f} ms wall/step")
 
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * 2**20 // 4
@@ -256,6 +282,7 @@ def main() -> None:
         "kernel": "forward_kernel",
         "flop_per_launch": FLOP_PER_POINT_FORWARD * args.points,
         "avg_launch_ms": round(fwd_kernel_ms, 5),
+        "avg_launch_ms_from": "HIP events on the launch stream around the timed calls, divided by the call count",
     }
     roofline_backward = {
         "bound": "mfma",

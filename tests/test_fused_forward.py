@@ -87,6 +87,25 @@ def test_forward_is_bitwise_reproducible_and_version_independent() -> None:
         assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
 
 
+@pytest.mark.parametrize("batch", [1000, 65536])
+def test_forward_workgroup_shape_does_not_change_results(batch: int) -> None:
+    """12 waves per workgroup (default) and 8 (FUSED_HOAD_FWD_WAVES=8) only distribute tiles
+    differently; every tile's arithmetic is the same, so the outputs are bitwise equal."""
+    import os
+
+    announce(f"forward 12-wave vs 8-wave workgroups, batch={batch}")
+    p = packed(0)
+    x = coordinates(batch, seed=17)
+    u12, l12 = _fused(x, p)
+    os.environ["FUSED_HOAD_FWD_WAVES"] = "8"
+    try:
+        u8, l8 = _fused(x, p)
+    finally:
+        del os.environ["FUSED_HOAD_FWD_WAVES"]
+    torch.cuda.synchronize()
+    assert torch.equal(u12, u8) and torch.equal(l12, l8)
+
+
 def test_forward_handles_empty_batch() -> None:
     announce("forward, empty batch")
     u, lap = _fused(torch.empty(0, 2, device="cuda"), packed(0))
