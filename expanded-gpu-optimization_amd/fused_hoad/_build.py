@@ -30,6 +30,9 @@ LIBRARY = PACKAGE_DIR / LIBRARY_NAME
 ARCH = "gfx950"
 
 # -packed-fp32-ops keeps hipcc from forming v_pk_*_f32 instructions from scalar float code.
+# -amdgpu-mfma-vgpr-form has MFMAs write their results to VGPRs where registers allow, so the
+# VALU work that consumes them (tanh jet and adjoint) needs fewer AGPR-to-VGPR copies: in the
+# backward kernel, 364 copies instead of 764 and 10 % fewer VALU instructions.
 HIP_FLAGS = [
     "-O3",
     "-std=c++17",
@@ -38,6 +41,8 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-fPIC",
     "-shared",
 ]
