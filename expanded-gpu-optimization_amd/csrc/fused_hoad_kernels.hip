@@ -574,8 +574,10 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
 //      tanh-jet adjoint in registers, dW += zbar h_prev^T, hbar = W^T zbar (registers), and
 //      finally layer 0 in closed form;
 //   3. dW contracts over the points of all 4 waves: zbar and h_prev are staged in LDS (two
-//      components at a time) and wave w owns output rows 16 w .. 16 w + 15 of every dW.
-//      Bias, W0 and w_out gradients are reduced over points by the same owner waves.
+//      components at a time) and wave w owns output rows 16 w .. 16 w + 15 of every dW; the
+//      hidden bias gradients fall out of the same LDS reads. W0, b0 and w_out gradients are
+//      summed over each wave's points in registers (pick_row_sum) and over the 4 waves once
+//      per slot.
 // Weight gradients accumulate in registers across the tiles of a "slot": slot s takes the
 // workgroup tiles s, s + slots, s + 2 slots, ... in that order and writes one partial row.
 // A second kernel sums the rows in a fixed tree. The slot count depends only on the batch,
