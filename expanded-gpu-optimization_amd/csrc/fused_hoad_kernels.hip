@@ -713,6 +713,110 @@ __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&
   dw_product(stage_rows, w, dw);
 }
 
+// ---- value channel only (boundary tiles of the fused step) ----
+// The building blocks above restricted to jet component 0, with the same operand order, so
+// each accumulator sees the same sequence of MFMAs as its component-0 counterpart.
+
+// acc[mb] = bias[mb] + W[16 mb + ., :] hv: component 0 of hidden_product.
+__device__ __forceinline__ void hidden_product_value(const float* w, const f4 (&hv)[4],
+                                                     const f4 (&bias)[4], f4 (&acc)[4]) {
+  f4 next[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) next[mb] = lds4(w + 1088 * mb);
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) {
+    f4 a[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) a[mb] = next[mb];
+    if (ob < 3) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) next[mb] = lds4(w + 1088 * mb + 16 * (ob + 1));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma(a[mb][j], hv[ob][j], (ob | j) ? acc[mb] : bias[mb]);
+    }
+    if (ob < 3) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+  }
+}
+
+// hb[ib] = sum_o W[o][16 ib + .] zb[o]: component 0 of hidden_product_t.
+__device__ __forceinline__ void hidden_product_t_value(const float* w, const f4 (&zb)[4],
+                                                       f4 (&hb)[4]) {
+  float next[4];
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) next[ib] = w[16 * ib];
+#pragma unroll
+  for (int step = 0; step < 16; ++step) {
+    const int ob = step >> 2, j = step & 3;
+    float a[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) a[ib] = next[ib];
+    if (step < 15) {
+      const int nob = (step + 1) >> 2, nj = (step + 1) & 3;
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) next[ib] = w[1088 * nob + kWRow * nj + 16 * ib];
+    }
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      hb[ib] = mfma(a[ib], zb[ob][j], (ob | j) ? hb[ib] : f4{0.f, 0.f, 0.f, 0.f});
+    }
+    if (step < 15) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+  }
+}
+
+// dW += zbar_v h_v^T over the workgroup tile (planes 0 and 2 only: the cc = 0 half of
+// dw_product). Returns the sum of this lane's zbar_v reads.
+__device__ __forceinline__ float dw_product_value(const float* stage_rows, int w, f4 (&dw)[4]) {
+  float bias = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const f4 a = lds4(stage_rows + 1088 * w + 16 * s);
+    f4 b[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) b[nb] = lds4(stage_rows + 2 * kPlane + 1088 * nb + 16 * s);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      bias += a[k];
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) dw[nb] = mfma(a[k], b[nb][k], dw[nb]);
+    }
+  }
+  return bias;
+}
+
+// stage_and_dw for the value channel: stages zbar_v and the previous layer's v = tanh(zp) (or,
+// with kFromLayer0, layer 0's), accumulates dW and the bias gradient, and returns the previous
+// layer's (v', s) in (pv, ps).
+template <bool kFromLayer0>
+__device__ __forceinline__ void stage_and_dw_value(const f4 (&zbar)[4], const f4 (&zp)[4],
+                                                   f4 (&dw)[4], float& g_bias, float* stage_lane,
+                                                   const float* stage_rows, const float* s_small,
+                                                   int w, int g, float x0, float x1, f4 (&pv)[4],
+                                                   f4 (&ps)[4]) {
+  __syncthreads();  // previous readers of the staging buffer are done
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    Layer0Weights w0;
+    if (kFromLayer0) w0 = layer0_weights(s_small, mb, g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v, sl;
+      tanh_scaled(kFromLayer0 ? layer0_zv(w0, r, x0, x1) : zp[mb][r], v, sl);
+      pv[mb][r] = v;
+      ps[mb][r] = sl;
+      float* p = stage_lane + 1088 * mb + kWRow * r;
+      p[0] = zbar[mb][r];
+      p[2 * kPlane] = v;
+    }
+  }
+  __syncthreads();
+  g_bias += sum_lane_groups(dw_product_value(stage_rows, w, dw));
+}
+
 // Seed of the fused Poisson training step (kLoss). The loss is the PINN loss
 //   mean_interior (lap - f)^2 + w mean_boundary u^2
 // (/root/reference/src/fused_hoad/training.py:66-88; with no boundary points, the loss of
@@ -736,6 +840,140 @@ struct LossSeed {
 
 constexpr int kLossColumn = kParameterCount;  // partial-row columns of sum r^2, sum u_b^2
 static_assert(kLossColumn + 1 < kRowStride, "the loss columns must fit in a partial row");
+
+// Per-slot gradient sums of one wave (see backward_kernel).
+struct WaveSums {
+  f4 dw[3][4];         // hidden dW, rows 16 w + ., in MFMA accumulator layout
+  float bh[3];         // hidden bias sums of c^-1 zbar_v (this lane's neuron, see dw_product)
+  float w0x, w0y, b0;  // layer-0 sums, lane = owned neuron
+  float wout, bout;    // output-layer sums
+  float loss, bloss;   // kLoss: sums of r^2 and u_b^2
+};
+
+// A boundary tile of the fused step. Boundary points enter the loss through u alone
+// (grad_lap = 0), so the output seed is (vbar, Jbar, Lbar) = (gu w_out / c, 0, 0), and the
+// tanh-jet adjoint maps (vbar, 0, 0, 0) to (s vbar, 0, 0, 0): every adjoint component but the
+// value one is exactly zero at every layer. The weight-gradient terms reduce to zbar_v h_v^T,
+// and the forward's J and L components feed nothing. This tile therefore runs the value
+// channel only, a quarter of the MFMA work of an interior tile; the terms it skips are exact
+// zeros. (The result can still differ from a full-jet run in the last bit: the full jet forms
+// some of these products as fma(a, b, 0), which the compiler cannot fuse into the row sums
+// that follow, and a plain a * b it may.)
+__device__ __forceinline__ void boundary_value_tile(const float* s_w, const float* s_small,
+                                                    float* s_stage, int rows_off, int cols_off,
+                                                    int stage_lane_off, int w, int g, int m_pick,
+                                                    float x0, float x1, bool active,
+                                                    float boundary_scale, WaveSums& acc) {
+  f4 hv[4], z1[4], z2[4], z3[4], bias[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const Layer0Weights w0 = layer0_weights(s_small, mb, g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v, s;
+      tanh_scaled(layer0_zv(w0, r, x0, x1), v, s);
+      hv[mb][r] = v;
+    }
+  }
+  load_bias(s_small, 0, g, bias);
+  hidden_product_value(s_w + opaque(rows_off), hv, bias, z1);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v, s;
+      tanh_scaled(z1[mb][r], v, s);
+      hv[mb][r] = v;
+    }
+  }
+  load_bias(s_small, 1, g, bias);
+  hidden_product_value(s_w + opaque(rows_off) + kPlane, hv, bias, z2);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v, s;
+      tanh_scaled(z2[mb][r], v, s);
+      hv[mb][r] = v;
+    }
+  }
+  load_bias(s_small, 2, g, bias);
+  hidden_product_value(s_w + opaque(rows_off) + 2 * kPlane, hv, bias, z3);
+  f4 tv[4], ts[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v, s;
+      tanh_scaled(z3[mb][r], v, s);
+      tv[mb][r] = v;
+      ts[mb][r] = s;
+    }
+  }
+
+  // u = w_out . v + b_out, the seed gu = fl(w / B_b) (2 u), and the output-layer sums.
+  float out = 0.0f;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const f4 wo = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) out = __builtin_fmaf(wo[r], tv[mb][r], out);
+  }
+  out = sum_lane_groups(out);
+  const float u = active ? out + s_small[kSmallBout] : 0.0f;
+  const float gu = boundary_scale * (2.0f * u);
+  acc.bloss += sum_row16(u * u);
+  const float gu_c = gu * (1.0f / kC);
+  f4 zb[4], hb[4];
+  {
+    float wout_sum = 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pick_row_sum(gu_c * tv[mb][r], 4 * mb + r, m_pick, wout_sum);
+        zb[mb][r] = ts[mb][r] * (gu * wv[r]);  // hidden layer 3's zbar_v = s vbar
+      }
+    }
+    acc.wout += wout_sum;
+    acc.bout += sum_row16(gu);
+  }
+
+  // Hidden layers 3, 2, 1: dW, then hbar_v = W^T zbar_v and the next zbar_v = s hbar_v.
+  stage_and_dw_value<false>(zb, z2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
+                            s_stage + opaque(rows_off), s_small, w, g, x0, x1, tv, ts);
+  hidden_product_t_value(s_w + opaque(cols_off) + 2 * kPlane, zb, hb);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) zb[mb] = ts[mb] * hb[mb];
+  stage_and_dw_value<false>(zb, z1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
+                            s_stage + opaque(rows_off), s_small, w, g, x0, x1, tv, ts);
+  hidden_product_t_value(s_w + opaque(cols_off) + kPlane, zb, hb);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) zb[mb] = ts[mb] * hb[mb];
+  stage_and_dw_value<true>(zb, z1, acc.dw[0], acc.bh[0], s_stage + opaque(stage_lane_off),
+                           s_stage + opaque(rows_off), s_small, w, g, x0, x1, tv, ts);
+  hidden_product_t_value(s_w + opaque(cols_off), zb, hb);
+
+  // Layer 0: bv = s hbar_v; dW0[o][d] = sum_p bv (c x_d), db0 = c sum_p bv.
+  {
+    float w0x_sum = 0.f, w0y_sum = 0.f, b0_sum = 0.f;
+    const float cx0 = kC * x0, cx1 = kC * x1;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float bv = ts[mb][r] * hb[mb][r];
+        pick_row_sum(bv * cx0, 4 * mb + r, m_pick, w0x_sum);
+        pick_row_sum(bv * cx1, 4 * mb + r, m_pick, w0y_sum);
+        pick_row_sum(bv, 4 * mb + r, m_pick, b0_sum);
+      }
+    }
+    acc.w0x += w0x_sum;
+    acc.w0y += w0y_sum;
+    acc.b0 += b0_sum;
+  }
+}
 
 // z of hidden layers 2 and 3 stays in registers through the walk back; z of hidden layer 1
 // would push the live state past the register file, so each wave parks it in its own 16 KB
@@ -773,29 +1011,38 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   const int64_t stash_off = static_cast<int64_t>(blockIdx.x * kBwdWaves + w) * kStashF4PerWave + lane;
 
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
-    f4 dw[3][4];
+    WaveSums acc;
 #pragma unroll
     for (int l = 0; l < 3; ++l) {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) dw[l][nb] = zero4();
+      for (int nb = 0; nb < 4; ++nb) acc.dw[l][nb] = zero4();
+      acc.bh[l] = 0.f;
     }
-    float g_bh[3] = {0.f, 0.f, 0.f};
-    float g_w0x = 0.f, g_w0y = 0.f, g_b0 = 0.f, g_wout = 0.f, g_bout = 0.f;
-    float g_loss = 0.f, g_bloss = 0.f;  // kLoss: this wave's sums of r^2 and u_b^2
+    acc.w0x = acc.w0y = acc.b0 = acc.wout = acc.bout = acc.loss = acc.bloss = 0.f;
 
     for (int64_t tile = slot; tile < tiles; tile += slots) {
       keep_lds_reads_in_loop();
       const int m_pick = opaque(m);  // pick_row_sum's 16 lane masks stay inside the tile
-      const bool on_boundary = kLoss && tile >= seed.interior_tiles;  // uniform per tile
-      const int64_t point = (on_boundary ? tile - seed.interior_tiles : tile) * kBwdTile + kTile * w + m;
-      const bool active = point < (on_boundary ? seed.boundary_count : batch);
-      const float* xy = on_boundary ? seed.boundary : coordinates;
+      if (kLoss && tile >= seed.interior_tiles) {  // boundary tile (uniform per workgroup)
+        const int64_t point = (tile - seed.interior_tiles) * kBwdTile + kTile * w + m;
+        const bool active = point < seed.boundary_count;
+        float x0 = 0.f, x1 = 0.f;
+        if (active) {
+          x0 = seed.boundary[2 * point];
+          x1 = seed.boundary[2 * point + 1];
+        }
+        boundary_value_tile(s_w, s_small, s_stage, rows_off, cols_off, stage_lane_off, w, g,
+                            m_pick, x0, x1, active, seed.boundary_scale, acc);
+        continue;
+      }
+      const int64_t point = tile * kBwdTile + kTile * w + m;
+      const bool active = point < batch;
       float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f, f = 0.f;
       if (active) {
-        x0 = xy[2 * point];
-        x1 = xy[2 * point + 1];
+        x0 = coordinates[2 * point];
+        x1 = coordinates[2 * point + 1];
         if (kLoss) {
-          if (!on_boundary) f = seed.source[point];
+          f = seed.source[point];
         } else {
           gu = grad_output[point];
           gl = grad_laplacian[point];
@@ -825,27 +1072,18 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       apply_tanh_jet_vs(z3, h, tv, ts);
 
       if (kLoss) {
-        // u = w_out . v + b_out (boundary) or lap = w_out . L (interior), in the forward
-        // kernel's order, then the seed.
+        // lap = w_out . L in the forward kernel's order, then the seed.
         float out = 0.0f;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
-          const f4 wo = lds4(s_small + (on_boundary ? kSmallWoutV : kSmallWoutL) + 16 * mb + 4 * g);
+          const f4 wo = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            out = __builtin_fmaf(wo[r], on_boundary ? h[mb][0][r] : h[mb][3][r], out);
-          }
+          for (int r = 0; r < 4; ++r) out = __builtin_fmaf(wo[r], h[mb][3][r], out);
         }
         out = sum_lane_groups(out);
-        if (on_boundary) {
-          const float u = active ? out + s_small[kSmallBout] : 0.0f;
-          gu = seed.boundary_scale * (2.0f * u);
-          g_bloss += sum_row16(u * u);
-        } else {
-          const float res = active ? out - f : 0.0f;
-          gl = seed.inv_batch * (2.0f * res);
-          g_loss += sum_row16(res * res);
-        }
+        const float res = active ? out - f : 0.0f;
+        gl = seed.inv_batch * (2.0f * res);
+        acc.loss += sum_row16(res * res);
       }
 
       // ---- 2. output layer: w_out / b_out gradients and the adjoint seed ----
@@ -871,13 +1109,13 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
             hb[mb][3][r] = gl * wl[r];
           }
         }
-        g_wout += wout_sum;
-        g_bout += sum_row16(gu);
+        acc.wout += wout_sum;
+        acc.bout += sum_row16(gu);
       }
 
       // ---- 3. hidden layer 3 ----
       tanh_adjoint_in_place(z3, hb, tv, ts);
-      stage_and_dw<false>(z3, z2, dw[2], g_bh[2], s_stage + opaque(stage_lane_off),
+      stage_and_dw<false>(z3, z2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
                           s_stage + opaque(rows_off), s_small, w, g, x0, x1,
                           tv, ts);
       hidden_product_t(s_w + opaque(cols_off) + 2 * kPlane, z3, hb);
@@ -892,14 +1130,14 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         for (int c = 0; c < 4; ++c) z1[mb][c] = stash_ld[(4 * mb + c) * kWave];
       }
       tanh_adjoint_in_place(z2, hb, tv, ts);
-      stage_and_dw<false>(z2, z1, dw[1], g_bh[1], s_stage + opaque(stage_lane_off),
+      stage_and_dw<false>(z2, z1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
                           s_stage + opaque(rows_off), s_small, w, g, x0, x1,
                           tv, ts);
       hidden_product_t(s_w + opaque(cols_off) + kPlane, z2, hb);
 
       // ---- 5. hidden layer 1 ----
       tanh_adjoint_in_place(z1, hb, tv, ts);
-      stage_and_dw<true>(z1, z1, dw[0], g_bh[0], s_stage + opaque(stage_lane_off),
+      stage_and_dw<true>(z1, z1, acc.dw[0], acc.bh[0], s_stage + opaque(stage_lane_off),
                           s_stage + opaque(rows_off), s_small, w, g, x0, x1,
                          tv, ts);
       hidden_product_t(s_w + opaque(cols_off), z1, hb);
@@ -924,12 +1162,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
             pick_row_sum(bv, 4 * mb + r, m_pick, b0_sum);                              // db0[o] / c
           }
         }
-        g_w0x += w0x_sum;
-        g_w0y += w0y_sum;
-        g_b0 += b0_sum;
+        acc.w0x += w0x_sum;
+        acc.w0y += w0y_sum;
+        acc.b0 += b0_sum;
         gx0 = sum_lane_groups(gx0);
         gx1 = sum_lane_groups(gx1);
-        if (g == 0 && active && (!kLoss || (grad_coordinates != nullptr && !on_boundary))) {
+        if (g == 0 && active && (!kLoss || grad_coordinates != nullptr)) {
           grad_coordinates[2 * point] = gx0;
           grad_coordinates[2 * point + 1] = gx1;
         }
@@ -945,23 +1183,23 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = dw[l][nb][r];
+        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = acc.dw[l][nb][r];
       }
-      if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * g_bh[l];  // bias sums are of c^-1 zbar_v
+      if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * acc.bh[l];  // bias sums are of c^-1 zbar_v
     }
     // Per-wave sums (lane = owned neuron) combined over the 4 waves in a fixed order.
     __syncthreads();  // every wave is done with the staging buffer
     {
       float* comb = s_stage;  // [quantity][wave][neuron]
       const int o = owned_neuron(m, g);
-      comb[(0 * kBwdWaves + w) * kHidden + o] = g_w0x;
-      comb[(1 * kBwdWaves + w) * kHidden + o] = g_w0y;
-      comb[(2 * kBwdWaves + w) * kHidden + o] = g_b0;
-      comb[(3 * kBwdWaves + w) * kHidden + o] = g_wout;
+      comb[(0 * kBwdWaves + w) * kHidden + o] = acc.w0x;
+      comb[(1 * kBwdWaves + w) * kHidden + o] = acc.w0y;
+      comb[(2 * kBwdWaves + w) * kHidden + o] = acc.b0;
+      comb[(3 * kBwdWaves + w) * kHidden + o] = acc.wout;
       if (lane == 0) {
-        s_red[0][w] = g_bout;
-        s_red[1][w] = g_loss;
-        s_red[2][w] = g_bloss;
+        s_red[0][w] = acc.bout;
+        s_red[1][w] = acc.loss;
+        s_red[2][w] = acc.bloss;
       }
       __syncthreads();
       const int q = threadIdx.x >> 6, n = threadIdx.x & 63;  // quantity (0..3), neuron
