@@ -140,13 +140,6 @@ __device__ __forceinline__ void tanh_jet_adjoint_vs(float v, float s, float zj0,
   bl = s * bl;
 }
 
-__device__ __forceinline__ void tanh_jet_adjoint(float zv, float zj0, float zj1, float zl,
-                                                 float& bv, float& bj0, float& bj1, float& bl) {
-  float v, s;
-  tanh_scaled(zv, v, s);
-  tanh_jet_adjoint_vs(v, s, zj0, zj1, zl, bv, bj0, bj1, bl);
-}
-
 // Small-parameter staging shared by both kernels (see kSmallCwx for the scaled forms).
 __device__ __forceinline__ void stage_small(const float* __restrict__ params, float* s_small,
                                             int tid, int threads) {
@@ -1374,6 +1367,14 @@ int current_device_cus(int* cus) {
   return FHOAD_SUCCESS;
 }
 
+// The stash part of the workspace is read and written as 16-byte vectors.
+int check_workspace_alignment(const void* workspace) {
+  if (reinterpret_cast<uintptr_t>(workspace) % alignof(f4) != 0) {
+    return fail(FHOAD_ERROR_MISALIGNED, "workspace must be 16-byte aligned");
+  }
+  return FHOAD_SUCCESS;
+}
+
 int64_t backward_tiles(int64_t batch) { return (batch + kBwdTile - 1) / kBwdTile; }
 
 int slots_for_tiles(int64_t tiles) { return static_cast<int>(std::min<int64_t>(tiles, kMaxSlots)); }
@@ -1486,6 +1487,7 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
     return fail(FHOAD_ERROR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes,
                 needed);
   }
+  if (int st = check_workspace_alignment(workspace)) return st;
   const int slots = backward_slots(batch);
   int grid = 0;
   if (int st = backward_grid(slots, &grid)) return st;
@@ -1526,6 +1528,7 @@ extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* so
     return fail(FHOAD_ERROR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes,
                 needed);
   }
+  if (int st = check_workspace_alignment(workspace)) return st;
   const int64_t interior_tiles = backward_tiles(batch);
   const int64_t tiles = interior_tiles + backward_tiles(boundary_count);
   const int slots = slots_for_tiles(tiles);

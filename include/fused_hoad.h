@@ -33,7 +33,7 @@ typedef enum fhoad_status {
   FHOAD_SUCCESS = 0,
   FHOAD_ERROR_INVALID_VERSION = 1,   /* version outside the accepted range */
   FHOAD_ERROR_INVALID_VALUE = 2,     /* null pointer or negative batch */
-  FHOAD_ERROR_MISALIGNED = 3,        /* reserved: no entry point requires more than float alignment */
+  FHOAD_ERROR_MISALIGNED = 3,        /* workspace not 16-byte aligned */
   FHOAD_ERROR_WORKSPACE = 4,         /* workspace missing or smaller than required */
   FHOAD_ERROR_DEVICE = 5             /* the HIP runtime reported an error */
 } fhoad_status;
@@ -73,7 +73,8 @@ size_t fhoad_backward_workspace_size(int64_t batch);
  * dLoss/dLaplacian (grad_laplacian[batch]), writes dLoss/dparameters (grad_parameters[12737],
  * overwritten, not accumulated) and dLoss/dcoordinates (grad_coordinates[batch][2]).
  * workspace must hold
- * fhoad_backward_workspace_size(batch) bytes (its contents on entry are ignored). The
+ * fhoad_backward_workspace_size(batch) bytes and be 16-byte aligned (hipMalloc and torch
+ * allocations are); its contents on entry are ignored. The
  * weight-gradient sum runs in a fixed order that does not depend on the grid size, so
  * results are bitwise reproducible. version 1..6 is accepted for API compatibility and every
  * value runs the same gfx950 kernels. batch == 0 zero-fills grad_parameters.
@@ -114,7 +115,8 @@ size_t fhoad_poisson_adam_step_workspace_size(int64_t batch, int64_t boundary_co
  *   loss: one float, written with the loss of the parameters on entry.
  *   grad_parameters: optional [12737] copy of the summed gradient (NULL: not written).
  *   grad_coordinates: optional [batch][2] dLoss/d(interior coordinates) (NULL: not written).
- *   workspace: fhoad_poisson_adam_step_workspace_size(batch, boundary_count) bytes.
+ *   workspace: fhoad_poisson_adam_step_workspace_size(batch, boundary_count) bytes, 16-byte
+ *     aligned.
  * Results are bitwise reproducible and do not depend on the grid size. batch must be > 0
  * (the loss of an empty interior set is undefined).
  *

@@ -125,6 +125,13 @@ def test_argument_errors_are_reported_before_any_device_work() -> None:
     assert call(fake, 16, None, 0, -1.0, 1 << 30, *adam) == 2
     assert call(fake, 16, None, 0, 100.0, 10, *adam) == 4
     assert call(fake, 16, fake, 300, 100.0, lib.fhoad_poisson_adam_step_workspace_size(16, 200), *adam) == 4
+    # The workspace holds 16-byte vectors: a pointer off that alignment is refused.
+    odd = ctypes.c_void_p(260)
+    assert step(fake, fake, 16, None, 0, 100.0, *[fake] * 5, None, None, odd, 1 << 30, *adam, None) == 3
+    assert b"16-byte aligned" in lib.fhoad_last_error()
+    backward = lib.fhoad_forward_laplacian_backward
+    assert backward(fake, fake, fake, fake, fake, fake, odd, 1 << 30, 16, 6, None) == 3
+    assert b"16-byte aligned" in lib.fhoad_last_error()
 
 
 def test_torch_extension_reports_contract_errors_on_cpu() -> None:
