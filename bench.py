@@ -269,9 +269,11 @@ def main() -> None:
     clock = _gpu_clock_mhz()
     fwd_tflops = FLOP_PER_POINT_FORWARD * args.points / (fwd_kernel_ms / 1e3) / 1e12
     bwd_tflops = FLOP_PER_POINT_BACKWARD * args.train_points / (bwd_ms / 1e3) / 1e12
-    traffic = None
+    traffic = None  # measured HBM bytes per launch, known only for the profiled workload
     if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+        measured = json.loads(TRAFFIC_FILE.read_text())
+        if measured.get("points") == args.points:
+            traffic = measured.get("hbm_bytes_per_launch")
     roofline = {
         "bound": "mfma",
         "achieved": round(fwd_tflops, 3),
