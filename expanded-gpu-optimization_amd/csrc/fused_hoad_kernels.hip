@@ -32,7 +32,8 @@
 // the jet update is MFMA time recovered.
 //
 // LDS weight layouts. The forward kernel keeps W in MFMA operand order (one 16-byte read per
-// k-step, see stage_operand_weights). The backward needs both W and W^T operands from one copy:
+// k-step, see stage_operand_weights); its small-batch form (forward_split_kernel) keeps only a
+// wave's 16 rows, in registers. The backward needs both W and W^T operands from one copy:
 // W[o][i] at 68 o + i, read as W[16 mb + m][16 ob + 4 g + j], j = 0..3 (16 bytes) for the forward
 // recompute and as W[16 ob + 4 g + j][16 ib + m] (4 bytes) for W^T zbar.
 #include <hip/hip_runtime.h>
@@ -551,6 +552,123 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
     if (g == 0 && active) {
       output[point] = u + s_small[kSmallBout];
       laplacian[point] = lap;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Small-batch forward. With fewer tiles than SIMDs, forward_kernel's call time is one tile's
+// latency: 768 dependent MFMAs on one wave. Here a workgroup of 4 waves (one per SIMD) runs one
+// 16-point tile at a time, and wave w computes output rows 16 w .. 16 w + 15 of every layer
+// (64 MFMAs per layer instead of 256). The tanh-jet outputs go through LDS to the other waves,
+// which need all 64 rows as the next layer's B operand. In forward_kernel's register layout the
+// B operand of k-step (ob, j) is register j of accumulator (ob, c) of the same lane, so the
+// exchange is lane to lane: each wave stores its 4 f4 per lane and reads the other waves' f4
+// at the same lane index (1 KB contiguous per wave access, no bank conflicts). Two LDS buffers
+// alternate, so one barrier per layer suffices.
+//
+// Wave w's chains are forward_kernel's accumulators (mb = w, c) with the same operands in the
+// same order, layer 0 is the same closed form, and wave 0 forms u and lap in forward_kernel's
+// order, so both kernels give bitwise the same results.
+constexpr int kSplitWaves = 4;
+
+__global__ void __launch_bounds__(kSplitWaves * kWave)
+forward_split_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
+                     float* __restrict__ output, float* __restrict__ laplacian, int64_t batch,
+                     int64_t tiles) {
+  __shared__ f4 s_h[2][kSplitWaves][4][kWave];  // [buffer][wave][component][lane], 32 KB
+  __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
+  stage_small(params, s_small, threadIdx.x, kSplitWaves * kWave);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int m = lane & 15;
+  const int g = lane >> 4;
+  // A operands of this wave's rows: wa[l][ob][j] = W_l[16 w + m][16 ob + 4 g + j], loaded once
+  // (global memory, L2-resident) instead of staging the whole matrix in LDS.
+  f4 wa[3][4];
+  {
+    const float* row = params + kHiddenBase + (16 * w + m) * kHidden + 4 * g;
+    const bool aligned = (reinterpret_cast<uintptr_t>(params) & 15) == 0;
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) {
+        const float* p = row + l * kHiddenStride + 16 * ob;
+        wa[l][ob] = aligned ? *reinterpret_cast<const f4*>(p) : f4{p[0], p[1], p[2], p[3]};
+      }
+    }
+  }
+  __syncthreads();  // s_small
+
+  int phase = 0;  // alternates the exchange buffers across layers and tiles
+  for (int64_t tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    keep_lds_reads_in_loop();
+    const int64_t point = tile * kTile + m;
+    const bool active = point < batch;
+    float x0 = 0.0f, x1 = 0.0f;
+    if (active) {
+      x0 = coordinates[2 * point];
+      x1 = coordinates[2 * point + 1];
+    }
+    f4 h[4][4];
+    layer0_forward(s_small, g, x0, x1, h);
+#pragma unroll
+    for (int layer = 0; layer < 3; ++layer) {
+      const f4 bias = lds4(s_small + kSmallBh + layer * kHidden + 16 * w + 4 * g);
+      f4 acc[4];
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const f4 cin = (ob | j) ? acc[c] : (c == 0 ? bias : f4{0.f, 0.f, 0.f, 0.f});
+            acc[c] = mfma(wa[layer][ob][j], h[ob][c][j], cin);
+          }
+        }
+      }
+      f4 mine[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v, j0, j1, l;
+        tanh_jet(acc[0][r], acc[1][r], acc[2][r], acc[3][r], v, j0, j1, l);
+        mine[0][r] = v;
+        mine[1][r] = j0;
+        mine[2][r] = j1;
+        mine[3][r] = l;
+      }
+      f4 (*buf)[4][kWave] = s_h[phase];
+      phase ^= 1;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) buf[w][c][lane] = mine[c];
+      __syncthreads();
+      if (layer < 2 || w == 0) {  // after the last layer only wave 0 (the output) reads
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) h[ob][c] = ob == w ? mine[c] : buf[ob][c][lane];
+        }
+      }
+    }
+    if (w == 0) {
+      float u = 0.0f, lap = 0.0f;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+        const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          u = __builtin_fmaf(wv[r], h[mb][0][r], u);
+          lap = __builtin_fmaf(wl[r], h[mb][3][r], lap);
+        }
+      }
+      u = sum_lane_groups(u);
+      lap = sum_lane_groups(lap);
+      if (g == 0 && active) {
+        output[point] = u + s_small[kSmallBout];
+        laplacian[point] = lap;
+      }
     }
   }
 }
@@ -1326,6 +1444,7 @@ __global__ void fill_zero_kernel(float* __restrict__ out, int64_t n) {
 // Forward workgroup: 12 waves, 3 per SIMD (150 VGPRs each). Measured against 8 waves: 3 % faster
 // at 64K points, 5 % at 256K; a CU's 16 tiles per 64K still split 4 per SIMD.
 constexpr int kFwdWaves = 12;
+constexpr int kSplitTilesPerCu = 2;  // forward_split_kernel up to this many tiles per CU
 
 thread_local char g_last_error[512] = "";
 
@@ -1439,9 +1558,19 @@ extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* pa
   if (int st = current_device_cus(&cus)) return st;
   const int64_t tiles = (batch + kTile - 1) / kTile;
   const int grid = static_cast<int>(std::min<int64_t>(tiles, cus));
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  // Below kSplitTilesPerCu tiles per CU the split kernel runs each tile on a CU's 4 SIMDs.
+  // FUSED_HOAD_FWD_SPLIT=0 / 1 (experiment knob, read per call) forces either kernel.
+  const char* split_env = std::getenv("FUSED_HOAD_FWD_SPLIT");
+  const bool split = split_env ? std::atoi(split_env) != 0 : tiles <= kSplitTilesPerCu * cus;
+  if (split) {
+    const int split_grid = static_cast<int>(std::min<int64_t>(tiles, kSplitTilesPerCu * cus));
+    hipLaunchKernelGGL(forward_split_kernel, dim3(split_grid), dim3(kSplitWaves * kWave), 0, hs,
+                       coordinates, parameters, output, laplacian, batch, tiles);
+    return check_launch("forward_split_kernel");
+  }
   // FUSED_HOAD_FWD_WAVES=8 (experiment knob, read per call) selects 8 waves per workgroup.
   const char* env = std::getenv("FUSED_HOAD_FWD_WAVES");
-  const hipStream_t hs = static_cast<hipStream_t>(stream);
   if (env && std::atoi(env) == 8) {
     hipLaunchKernelGGL(forward_kernel<8>, dim3(grid), dim3(8 * kWave), 0, hs, coordinates,
                        parameters, output, laplacian, batch, tiles);

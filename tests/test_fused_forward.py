@@ -8,6 +8,9 @@ max |error| <= 1e-4 max |expected| (test_fused.py:38-49).
 
 from __future__ import annotations
 
+import contextlib
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -87,23 +90,54 @@ def test_forward_is_bitwise_reproducible_and_version_independent() -> None:
         assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
 
 
+@contextlib.contextmanager
+def _env(**values: str):
+    """Set the kernels' experiment knobs (read per call) for the duration of a block."""
+    saved = {k: os.environ.get(k) for k in values}
+    os.environ.update(values)
+    try:
+        yield
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
 @pytest.mark.parametrize("batch", [1000, 65536])
 def test_forward_workgroup_shape_does_not_change_results(batch: int) -> None:
     """12 waves per workgroup (default) and 8 (FUSED_HOAD_FWD_WAVES=8) only distribute tiles
     differently; every tile's arithmetic is the same, so the outputs are bitwise equal."""
-    import os
-
     announce(f"forward 12-wave vs 8-wave workgroups, batch={batch}")
     p = packed(0)
     x = coordinates(batch, seed=17)
-    u12, l12 = _fused(x, p)
-    os.environ["FUSED_HOAD_FWD_WAVES"] = "8"
-    try:
-        u8, l8 = _fused(x, p)
-    finally:
-        del os.environ["FUSED_HOAD_FWD_WAVES"]
+    with _env(FUSED_HOAD_FWD_SPLIT="0"):
+        u12, l12 = _fused(x, p)
+        with _env(FUSED_HOAD_FWD_WAVES="8"):
+            u8, l8 = _fused(x, p)
     torch.cuda.synchronize()
     assert torch.equal(u12, u8) and torch.equal(l12, l8)
+
+
+@pytest.mark.parametrize(
+    "batch,scale",
+    [(1, 1.0), (15, 1.0), (16, 1.0), (17, 1.0), (1000, 1.0), (4096, 1.0), (8192, 3.0), (20000, 1.0)],
+)
+def test_split_forward_is_bitwise_equal_to_the_tiled_kernel(batch: int, scale: float) -> None:
+    """The small-batch kernel (one tile over a workgroup's 4 waves, rows split by wave) runs
+    the tiled kernel's MFMA chains and tanh updates in the same order, so the outputs are
+    bitwise equal; 20000 points force several tiles per workgroup through its exchange
+    buffers, and scale 3 saturates the tanh."""
+    announce(f"forward split kernel vs tiled kernel, batch={batch}, weights x{scale}")
+    p = packed(0) * scale
+    x = coordinates(batch, seed=23)
+    with _env(FUSED_HOAD_FWD_SPLIT="0"):
+        u_tiled, l_tiled = _fused(x, p)
+    with _env(FUSED_HOAD_FWD_SPLIT="1"):
+        u_split, l_split = _fused(x, p)
+    torch.cuda.synchronize()
+    assert torch.equal(u_tiled, u_split) and torch.equal(l_tiled, l_split)
 
 
 def test_forward_handles_empty_batch() -> None:

@@ -1,5 +1,5 @@
 """A packed parameter buffer that is only 4-byte aligned (a view into a larger tensor, as a
-caller's flat optimizer buffer may be) takes the kernels' scalar staging path; the staged values
+caller's flat optimizer buffer may be) takes the kernels' scalar load paths; the loaded values
 are the same, so every result is bitwise equal to the 16-byte-aligned run."""
 
 from __future__ import annotations
@@ -20,15 +20,17 @@ def _misaligned_copy(p: torch.Tensor) -> torch.Tensor:
     return view
 
 
-def test_forward_and_backward_with_a_misaligned_parameter_buffer() -> None:
+@pytest.mark.parametrize("batch", [5000, 40000])
+def test_forward_and_backward_with_a_misaligned_parameter_buffer(batch: int) -> None:
+    """5000 points run the small-batch forward kernel, 40000 the tiled one."""
     require_gpu_extension()
-    announce("misaligned parameters: forward + backward vs aligned, batch=5000")
+    announce(f"misaligned parameters: forward + backward vs aligned, batch={batch}")
     from fused_hoad._extension import fused_forward_laplacian, fused_forward_laplacian_backward
 
     p = packed(0)
     q = _misaligned_copy(p)
-    x = coordinates(5000, seed=21)
-    gu, gl = upstream(5000, seed=21)
+    x = coordinates(batch, seed=21)
+    gu, gl = upstream(batch, seed=21)
     for a, b in zip(fused_forward_laplacian(x, p), fused_forward_laplacian(x, q)):
         assert torch.equal(a, b)
     for a, b in zip(fused_forward_laplacian_backward(x, p, gu, gl), fused_forward_laplacian_backward(x, q, gu, gl)):
