@@ -33,7 +33,8 @@
 //
 // LDS weight layouts. The forward kernel keeps W in MFMA operand order (one 16-byte read per
 // k-step, see stage_operand_weights); its small-batch form (forward_split_kernel) keeps only a
-// wave's 16 rows, in registers. The backward needs both W and W^T operands from one copy:
+// wave's 16 rows, in registers. The backward kernels (backward_kernel, and
+// backward_split_kernel for small batches) need both W and W^T operands from one copy:
 // W[o][i] at 68 o + i, read as W[16 mb + m][16 ob + 4 g + j], j = 0..3 (16 bytes) for the forward
 // recompute and as W[16 ob + 4 g + j][16 ib + m] (4 bytes) for W^T zbar.
 #include <hip/hip_runtime.h>
@@ -425,21 +426,25 @@ __device__ __forceinline__ void apply_tanh_jet_vs(const f4 (&z)[4][4], f4 (&h)[4
 
 // Layer 0 in closed form: the input jet is (x, I, 0), so z_J = W0 columns and z_L = 0, and
 // the tanh jet's q = |z_J|^2 is a per-neuron constant.
+// One block: the jet of neurons 16 mb + 4 g + r, r = 0..3, in h[c][r].
+__device__ __forceinline__ void layer0_block(const float* s_small, int mb, int g, float x0,
+                                             float x1, f4 (&h)[4]) {
+  const Layer0Weights w = layer0_weights(s_small, mb, g);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v, s;
+    tanh_scaled(layer0_zv(w, r, x0, x1), v, s);
+    h[0][r] = v;
+    h[1][r] = s * w.wx[r];
+    h[2][r] = s * w.wy[r];
+    h[3][r] = s * (v * w.q[r]);
+  }
+}
+
 __device__ __forceinline__ void layer0_forward(const float* s_small, int g, float x0, float x1,
                                                f4 (&h)[4][4]) {
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const Layer0Weights w = layer0_weights(s_small, mb, g);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v, s;
-      tanh_scaled(layer0_zv(w, r, x0, x1), v, s);
-      h[mb][0][r] = v;
-      h[mb][1][r] = s * w.wx[r];
-      h[mb][2][r] = s * w.wy[r];
-      h[mb][3][r] = s * (v * w.q[r]);
-    }
-  }
+  for (int mb = 0; mb < 4; ++mb) layer0_block(s_small, mb, g, x0, x1, h[mb]);
 }
 
 // An opaque copy of a value: the compiler cannot see that it equals the input, so it cannot
@@ -1328,6 +1333,314 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Small-batch backward. backward_kernel carries 16 points per wave through the whole walk:
+// 2,304 dependent MFMAs per 64-point workgroup tile, so a batch with at most one workgroup
+// tile per CU costs that latency whatever its size. Here a workgroup of 4 waves runs one
+// 16-point tile at a time and wave w owns rows 16 w .. 16 w + 15 of every layer: 64 MFMAs per
+// layer for the forward re-run, 64 for dW and 64 for W^T zbar (576 per tile and wave).
+//   * Layer outputs h and adjoints zbar go to the other waves lane to lane through LDS
+//     (s_x, the register layout of forward_split_kernel), for the next product's B operand.
+//   * dW contracts over the tile's points, which sit on the lane axis: h (all 64 rows, per
+//     layer) and this wave's zbar are also stored transposed, [row][c][4 g + s] for point
+//     4 s + g at pitch 68, so one 16-byte read gives a lane 4 points of one (row, c).
+//   * Each wave owns distinct entries of the slot's partial row (its rows of every block), so
+//     the partial row needs no combine across waves.
+// Slots and the fixed-order reduction are those of backward_kernel with 16-point tiles. The
+// choice between the two kernels depends only on the batch, so results do not depend on the
+// device. The tanh-jet, adjoint and loss arithmetic is backward_kernel's; the sums over points
+// are grouped differently, so the two kernels agree to rounding, not bitwise.
+constexpr int kSplitBwdMaxTiles = 768;  // backward_split_kernel up to 768 16-point tiles
+constexpr int kTPlane = 64 * kWRow;     // floats of one transposed 64-row layer (h)
+constexpr int kTWave = 16 * kWRow;      // floats of one wave's transposed zbar
+
+// Store this lane's 4 rows (rows0 + 4 g + r) x 4 components at point m into a transposed
+// buffer t[row][68]: component c of point p = 4 s + g' at t[row * 68 + 16 c + 4 g' + s].
+__device__ __forceinline__ void store_transposed(float* t, int rows0, int g, int m,
+                                                 const f4 (&x)[4]) {
+  const int col = 4 * (m & 3) + (m >> 2);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) t[(rows0 + 4 * g + r) * kWRow + 16 * c + col] = x[c][r];
+  }
+}
+
+template <bool kLoss>
+__global__ void __launch_bounds__(kSplitWaves * kWave, 1)
+backward_split_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
+                      const float* __restrict__ grad_output,
+                      const float* __restrict__ grad_laplacian,
+                      float* __restrict__ grad_coordinates, float* __restrict__ partials,
+                      int64_t batch, int64_t tiles, int slots, LossSeed seed) {
+  __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
+  __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
+  __shared__ __attribute__((aligned(16))) float s_ht[3 * kTPlane];  // h0, h1, h2 transposed
+  __shared__ f4 s_x[2][kSplitWaves][4][kWave];                       // lane-major exchange
+  __shared__ __attribute__((aligned(16))) float s_zt[kSplitWaves][kTWave];
+  __shared__ float s_gx[kSplitWaves][2][kTile];
+  if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] += 1.0f;
+  stage_parameters<kSplitWaves * kWave>(params, s_w, s_small, threadIdx.x);
+  __syncthreads();
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  const int m = lane & 15;
+  const int g = lane >> 4;
+  const int rows_off = lane_rows(m, g) + 1088 * w;  // W[16 w + m][.] (forward operand)
+  const int cols_off = lane_cols(m, g) + 16 * w;    // W[.][16 w + m] (transposed operand)
+  const int t_read = m * kWRow + 4 * g;             // transposed reads: row m, points 4 s + g
+
+  int phase = 0;  // alternates the s_x buffers
+  for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
+    f4 dw[3][4];
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) dw[l][nb] = zero4();
+    }
+    // Per-lane sums: bias[l] of row 16 w + m (all lane groups), the others of row
+    // 16 w + 4 g + (m & 3).
+    float bias[3] = {0.f, 0.f, 0.f};
+    float g_w0x = 0.f, g_w0y = 0.f, g_b0 = 0.f, g_wout = 0.f, g_bout = 0.f;
+    float g_loss = 0.f, g_bloss = 0.f;
+
+    for (int64_t tile = slot; tile < tiles; tile += slots) {
+      keep_lds_reads_in_loop();
+      const bool on_boundary = kLoss && tile >= seed.interior_tiles;  // uniform per workgroup
+      const int64_t point = (on_boundary ? tile - seed.interior_tiles : tile) * kTile + m;
+      const bool active = point < (on_boundary ? seed.boundary_count : batch);
+      const float* xy = on_boundary ? seed.boundary : coordinates;
+      float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f, f = 0.f;
+      if (active) {
+        x0 = xy[2 * point];
+        x1 = xy[2 * point + 1];
+        if (kLoss) {
+          if (!on_boundary) f = seed.source[point];
+        } else {
+          gu = grad_output[point];
+          gl = grad_laplacian[point];
+        }
+      }
+
+      // ---- forward re-run: all 64 rows of layer 0, then this wave's rows of layers 1..3 ----
+      f4 h[4][4];
+      layer0_forward(s_small, g, x0, x1, h);
+      {
+        f4 own[4];  // this wave's block again (h[w] would need a dynamic register index)
+        layer0_block(s_small, w, g, x0, x1, own);
+        store_transposed(s_ht, 16 * w, g, m, own);
+      }
+      f4 z[3][4];  // this wave's pre-activations of hidden layers 1..3
+      f4 mine[4];  // this wave's rows of the current layer output
+#pragma unroll
+      for (int layer = 0; layer < 3; ++layer) {
+        const f4 b = lds4(s_small + kSmallBh + layer * kHidden + 16 * w + 4 * g);
+        const float* wrow = s_w + layer * kPlane + opaque(rows_off);
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) {
+          const f4 a = lds4(wrow + 16 * ob);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const f4 cin = (ob | j) ? z[layer][c] : (c == 0 ? b : zero4());
+              z[layer][c] = mfma(a[j], h[ob][c][j], cin);
+            }
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v, j0, j1, l;
+          tanh_jet(z[layer][0][r], z[layer][1][r], z[layer][2][r], z[layer][3][r], v, j0, j1, l);
+          mine[0][r] = v;
+          mine[1][r] = j0;
+          mine[2][r] = j1;
+          mine[3][r] = l;
+        }
+        f4 (*xb)[4][kWave] = s_x[phase];
+        phase ^= 1;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xb[w][c][lane] = mine[c];
+        if (layer < 2) store_transposed(s_ht + (layer + 1) * kTPlane, 16 * w, g, m, mine);
+        __syncthreads();
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) h[ob][c] = xb[ob][c][lane];  // this wave's block included
+        }
+      }
+
+      if (kLoss) {
+        // u (boundary) or lap (interior) over all 64 rows, in backward_kernel's order.
+        float out = 0.0f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const f4 wo = lds4(s_small + (on_boundary ? kSmallWoutV : kSmallWoutL) + 16 * mb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            out = __builtin_fmaf(wo[r], on_boundary ? h[mb][0][r] : h[mb][3][r], out);
+          }
+        }
+        out = sum_lane_groups(out);
+        if (on_boundary) {
+          const float u = active ? out + s_small[kSmallBout] : 0.0f;
+          gu = seed.boundary_scale * (2.0f * u);
+          g_bloss += sum_row16(u * u);
+        } else {
+          const float res = active ? out - f : 0.0f;
+          gl = seed.inv_batch * (2.0f * res);
+          g_loss += sum_row16(res * res);
+        }
+      }
+
+      // ---- output layer: this wave's rows of the seed and of dw_out ----
+      f4 hb[4];
+      {
+        const float gu_c = gu * (1.0f / kC);
+        const float gl_l = gl * (1.0f / kLambda);
+        const f4 wv = lds4(s_small + kSmallWoutV + 16 * w + 4 * g);
+        const f4 wl = lds4(s_small + kSmallWoutL + 16 * w + 4 * g);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float total = sum_row16(__builtin_fmaf(gu_c, mine[0][r], gl_l * mine[3][r]));
+          g_wout = (m & 3) == r ? g_wout + total : g_wout;
+          hb[0][r] = gu * wv[r];
+          hb[1][r] = 0.0f;
+          hb[2][r] = 0.0f;
+          hb[3][r] = gl * wl[r];
+        }
+        g_bout += sum_row16(gu);
+      }
+
+      // ---- hidden layers 3, 2, 1 ----
+#pragma unroll
+      for (int layer = 2; layer >= 0; --layer) {
+        // zbar of this wave's rows (tanh-jet adjoint, lane-local)
+        f4 zb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v, s;
+          tanh_scaled(z[layer][0][r], v, s);
+          float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
+          tanh_jet_adjoint_vs(v, s, z[layer][1][r], z[layer][2][r], z[layer][3][r], bv, bj0, bj1,
+                              bl);
+          zb[0][r] = bv;
+          zb[1][r] = bj0;
+          zb[2][r] = bj1;
+          zb[3][r] = bl;
+        }
+        f4 (*xb)[4][kWave] = s_x[phase];
+        phase ^= 1;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xb[w][c][lane] = zb[c];
+        float* zt = &s_zt[w][0];
+        store_transposed(zt, 0, g, m, zb);
+        __syncthreads();
+        // dW[16 w + ., 16 nb + .] += sum over (c, points) of zbar h_prev^T; the A reads of
+        // component 0 also give the bias sum of row 16 w + m.
+        {
+          const float* ht = s_ht + layer * kTPlane + opaque(t_read);
+          const float* za = zt + opaque(t_read);
+          float bsum = 0.0f;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const f4 a = lds4(za + 16 * c);
+            f4 bt[4];
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) bt[nb] = lds4(ht + 16 * kWRow * nb + 16 * c);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              if (c == 0) bsum += a[s];
+#pragma unroll
+              for (int nb = 0; nb < 4; ++nb) dw[layer][nb] = mfma(a[s], bt[nb][s], dw[layer][nb]);
+            }
+          }
+          bias[layer] += sum_lane_groups(bsum);
+        }
+        // hbar of this wave's rows of the layer below: sum over all 64 rows o of
+        // W[o][16 w + .] zbar[o].
+        {
+          const float* wt = s_w + layer * kPlane + opaque(cols_off);
+#pragma unroll
+          for (int ob = 0; ob < 4; ++ob) {
+            f4 zo[4];  // zbar of rows 16 ob .. 16 ob + 15 (this wave's block included)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) zo[c] = xb[ob][c][lane];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float a = wt[1088 * ob + kWRow * j];
+#pragma unroll
+              for (int c = 0; c < 4; ++c) hb[c] = mfma(a, zo[c][j], (ob | j) ? hb[c] : zero4());
+            }
+          }
+        }
+      }
+
+      // ---- layer 0 for this wave's rows: dW0, db0 and this wave's part of grad_x ----
+      {
+        const Layer0Weights w0 = layer0_weights(s_small, w, g);
+        const float cx0 = kC * x0, cx1 = kC * x1;
+        float gx0 = 0.f, gx1 = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v, s;
+          tanh_scaled(layer0_zv(w0, r, x0, x1), v, s);
+          float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
+          tanh_jet_adjoint_vs(v, s, w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
+          gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
+          gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
+          const float t0 = sum_row16(__builtin_fmaf(bv, cx0, bj0));
+          const float t1 = sum_row16(__builtin_fmaf(bv, cx1, bj1));
+          const float tb = sum_row16(bv);
+          g_w0x = (m & 3) == r ? g_w0x + t0 : g_w0x;
+          g_w0y = (m & 3) == r ? g_w0y + t1 : g_w0y;
+          g_b0 = (m & 3) == r ? g_b0 + tb : g_b0;
+        }
+        gx0 = sum_lane_groups(gx0);
+        gx1 = sum_lane_groups(gx1);
+        if (g == 0) {
+          s_gx[w][0][m] = gx0;
+          s_gx[w][1][m] = gx1;
+        }
+        __syncthreads();
+        if (w == 0 && g == 0 && active && (!kLoss || (grad_coordinates != nullptr && !on_boundary))) {
+          grad_coordinates[2 * point] = ((s_gx[0][0][m] + s_gx[1][0][m]) + s_gx[2][0][m]) + s_gx[3][0][m];
+          grad_coordinates[2 * point + 1] = ((s_gx[0][1][m] + s_gx[1][1][m]) + s_gx[2][1][m]) + s_gx[3][1][m];
+        }
+      }
+    }
+
+    // ---- this slot's partial row: each wave writes its own rows ----
+    float* row = partials + static_cast<int64_t>(slot) * kRowStride;
+    const int dw_lane = opaque((16 * w + 4 * g) * kHidden + m);
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+      float* wrow = row + kHiddenBase + l * kHiddenStride;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = dw[l][nb][r];
+      }
+      if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * bias[l];
+    }
+    if (m < 4) {
+      const int n = 16 * w + 4 * g + m;
+      row[kInputs * n] = g_w0x;
+      row[kInputs * n + 1] = g_w0y;
+      row[kLayer0Bias + n] = kC * g_b0;
+      row[kOutputBase + n] = g_wout;
+    }
+    if (w == 0 && lane == 0) {
+      row[kOutputBase + kHidden] = g_bout;
+      if (kLoss) {
+        row[kLossColumn] = g_loss;
+        row[kLossColumn + 1] = g_bloss;
+      }
+    }
+  }
+}
+
 // Column k's total over the slots, complete in the threads of group 0 (columns >= `columns`
 // read nothing and give 0).
 __device__ __forceinline__ float fixed_tree_sum(const float* __restrict__ partials, int slots,
@@ -1507,6 +1820,28 @@ size_t workspace_bytes_for(int slots) {
          (kRowStride * sizeof(float) + kBwdWaves * kStashF4PerWave * sizeof(f4));
 }
 
+int64_t split_tiles(int64_t points) { return (points + kTile - 1) / kTile; }
+
+// Gradient kernel for `batch` interior and `boundary_count` boundary points:
+// backward_split_kernel up to kSplitBwdMaxTiles 16-point tiles, chosen from the batch alone
+// so that results do not depend on the device. FUSED_HOAD_BWD_SPLIT=0 / 1 (experiment knob,
+// read per call) forces either kernel.
+bool use_split_backward(int64_t batch, int64_t boundary_count) {
+  if (const char* env = std::getenv("FUSED_HOAD_BWD_SPLIT")) return std::atoi(env) != 0;
+  return split_tiles(batch) + split_tiles(boundary_count) <= kSplitBwdMaxTiles;
+}
+
+// Workspace for either gradient kernel: the larger of backward_kernel's (partial rows and
+// stashes) and backward_split_kernel's (partial rows).
+size_t gradient_workspace_bytes(int64_t batch, int64_t boundary_count) {
+  const size_t tiled = workspace_bytes_for(
+      slots_for_tiles(backward_tiles(batch) + backward_tiles(boundary_count)));
+  const size_t split =
+      static_cast<size_t>(slots_for_tiles(split_tiles(batch) + split_tiles(boundary_count))) *
+      kRowStride * sizeof(float);
+  return std::max(tiled, split);
+}
+
 // Persistent grid of the gradient kernel: one workgroup per CU, at most one per slot.
 // FUSED_HOAD_BWD_BLOCKS caps it, as in the reference (fused_backward.cu:873-880). Here it
 // changes only which workgroup computes a slot, never the arithmetic, so gradients stay
@@ -1583,12 +1918,12 @@ extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* pa
 
 extern "C" size_t fhoad_backward_workspace_size(int64_t batch) {
   if (batch <= 0) return 0;
-  return workspace_bytes_for(backward_slots(batch));
+  return gradient_workspace_bytes(batch, 0);
 }
 
 extern "C" size_t fhoad_poisson_adam_step_workspace_size(int64_t batch, int64_t boundary_count) {
   if (batch <= 0 || boundary_count < 0) return 0;
-  return workspace_bytes_for(slots_for_tiles(backward_tiles(batch) + backward_tiles(boundary_count)));
+  return gradient_workspace_bytes(batch, boundary_count);
 }
 
 extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const float* parameters,
@@ -1617,15 +1952,25 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
                 needed);
   }
   if (int st = check_workspace_alignment(workspace)) return st;
-  const int slots = backward_slots(batch);
-  int grid = 0;
-  if (int st = backward_grid(slots, &grid)) return st;
   float* partials = static_cast<float*>(workspace);
-  f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
-  hipLaunchKernelGGL(backward_kernel<false>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
-                     coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
-                     partials, stash, batch, backward_tiles(batch), slots, LossSeed{});
-  if (int st = check_launch("backward_kernel")) return st;
+  int slots = 0, grid = 0;
+  if (use_split_backward(batch, 0)) {
+    const int64_t tiles = split_tiles(batch);
+    slots = slots_for_tiles(tiles);
+    if (int st = backward_grid(slots, &grid)) return st;
+    hipLaunchKernelGGL(backward_split_kernel<false>, dim3(grid), dim3(kSplitWaves * kWave), 0, hs,
+                       coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
+                       partials, batch, tiles, slots, LossSeed{});
+    if (int st = check_launch("backward_split_kernel")) return st;
+  } else {
+    slots = backward_slots(batch);
+    if (int st = backward_grid(slots, &grid)) return st;
+    f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
+    hipLaunchKernelGGL(backward_kernel<false>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
+                       coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
+                       partials, stash, batch, backward_tiles(batch), slots, LossSeed{});
+    if (int st = check_launch("backward_kernel")) return st;
+  }
   hipLaunchKernelGGL(reduce_partials_kernel, dim3((kParameterCount + 63) / 64),
                      dim3(kReduceGroups * 64), 0, hs, partials, slots, grad_parameters);
   return check_launch("reduce_partials_kernel");
@@ -1658,8 +2003,10 @@ extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* so
                 needed);
   }
   if (int st = check_workspace_alignment(workspace)) return st;
-  const int64_t interior_tiles = backward_tiles(batch);
-  const int64_t tiles = interior_tiles + backward_tiles(boundary_count);
+  const bool split = use_split_backward(batch, boundary_count);
+  const int64_t interior_tiles = split ? split_tiles(batch) : backward_tiles(batch);
+  const int64_t tiles =
+      interior_tiles + (split ? split_tiles(boundary_count) : backward_tiles(boundary_count));
   const int slots = slots_for_tiles(tiles);
   int grid = 0;
   if (int st = backward_grid(slots, &grid)) return st;
@@ -1669,12 +2016,19 @@ extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* so
   const float boundary_scale = boundary_count > 0 ? weight / static_cast<float>(boundary_count) : 0.0f;
   const float inv_boundary = boundary_count > 0 ? 1.0f / static_cast<float>(boundary_count) : 0.0f;
   float* partials = static_cast<float*>(workspace);
-  f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
   const LossSeed seed{source, boundary, interior_tiles, boundary_count, inv_batch, boundary_scale, step};
-  hipLaunchKernelGGL(backward_kernel<true>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
-                     coordinates, parameters, nullptr, nullptr, grad_coordinates, partials, stash,
-                     batch, tiles, slots, seed);
-  if (int st = check_launch("backward_kernel")) return st;
+  if (split) {
+    hipLaunchKernelGGL(backward_split_kernel<true>, dim3(grid), dim3(kSplitWaves * kWave), 0, hs,
+                       coordinates, parameters, nullptr, nullptr, grad_coordinates, partials,
+                       batch, tiles, slots, seed);
+    if (int st = check_launch("backward_split_kernel")) return st;
+  } else {
+    f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
+    hipLaunchKernelGGL(backward_kernel<true>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
+                       coordinates, parameters, nullptr, nullptr, grad_coordinates, partials,
+                       stash, batch, tiles, slots, seed);
+    if (int st = check_launch("backward_kernel")) return st;
+  }
   const AdamArgs args{parameters, exp_avg, exp_avg_sq, step, loss, grad_parameters,
                       lr, beta1, beta2, eps, weight_decay, inv_batch, inv_boundary, weight};
   hipLaunchKernelGGL(reduce_adam_kernel, dim3((kLossColumn + 2 + 63) / 64),

@@ -64,7 +64,8 @@ int fhoad_forward_laplacian(const float* coordinates, const float* parameters, f
 
 /*
  * Bytes of device workspace fhoad_forward_laplacian_backward needs for `batch` points
- * (per-slot weight-gradient partial rows). 0 for batch <= 0.
+ * (per-slot weight-gradient partial rows, plus per-wave stashes for large batches). It depends
+ * only on the batch. 0 for batch <= 0.
  */
 size_t fhoad_backward_workspace_size(int64_t batch);
 

@@ -4,6 +4,8 @@ the GPU."""
 
 from __future__ import annotations
 
+import contextlib
+import os
 import sys
 
 import numpy as np
@@ -42,3 +44,19 @@ def upstream(batch: int, seed: int = 0, device: str = "cuda"):
 
 def to_numpy64(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().double().numpy()
+
+
+@contextlib.contextmanager
+def knobs(**values: str):
+    """Set the kernels' experiment knobs (environment variables read on every call) for the
+    duration of a block, restoring the previous values afterwards."""
+    saved = {k: os.environ.get(k) for k in values}
+    os.environ.update(values)
+    try:
+        yield
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v

@@ -77,21 +77,30 @@ def test_constants_and_status_strings() -> None:
     assert lib.fhoad_status_string(4) == b"workspace too small"
 
 
-def test_workspace_size_is_one_partial_row_and_stash_per_slot() -> None:
+def _expected_workspace(batch: int, boundary: int = 0) -> int:
+    """Either gradient kernel may run (a knob can force either), so the workspace covers the
+    larger need: 64-point tiles with a partial row and four 16 KB wave stashes per slot, or
+    16-point tiles with a partial row per slot; at most 256 slots."""
+    row = 12800 * 4
+    tiled = min(256, -(-batch // 64) - (-boundary // 64)) * (row + 4 * 16 * 1024)
+    split = min(256, -(-batch // 16) - (-boundary // 16)) * row
+    return max(tiled, split)
+
+
+def test_workspace_size_covers_either_gradient_kernel() -> None:
     lib = _lib()
     assert lib.fhoad_backward_workspace_size(0) == 0
-    per_slot = 12800 * 4 + 4 * 16 * 1024  # partial row + four 16 KB per-wave stashes
+    per_slot = 12800 * 4 + 4 * 16 * 1024
     assert lib.fhoad_backward_workspace_size(1) == per_slot
-    assert lib.fhoad_backward_workspace_size(64) == per_slot
-    assert lib.fhoad_backward_workspace_size(65) == 2 * per_slot
     assert lib.fhoad_backward_workspace_size(65536) == 256 * per_slot
     assert lib.fhoad_backward_workspace_size(1 << 20) == 256 * per_slot
-    # the fused step's slots cover the interior tiles and the boundary tiles
+    for batch in (1, 16, 17, 64, 65, 1000, 4096, 12288, 12289, 20000):
+        assert lib.fhoad_backward_workspace_size(batch) == _expected_workspace(batch), batch
     assert lib.fhoad_poisson_adam_step_workspace_size(0, 5) == 0
-    assert lib.fhoad_poisson_adam_step_workspace_size(64, 0) == per_slot
-    assert lib.fhoad_poisson_adam_step_workspace_size(65, 1) == 3 * per_slot
-    assert lib.fhoad_poisson_adam_step_workspace_size(16384, 1024) == 256 * per_slot
-    assert lib.fhoad_poisson_adam_step_workspace_size(1000, 200) == (16 + 4) * per_slot
+    for batch, boundary in ((64, 0), (65, 1), (1000, 200), (16384, 1024), (12000, 300)):
+        assert lib.fhoad_poisson_adam_step_workspace_size(batch, boundary) == _expected_workspace(
+            batch, boundary
+        ), (batch, boundary)
 
 
 def test_argument_errors_are_reported_before_any_device_work() -> None:

@@ -17,7 +17,7 @@ import torch
 
 from conftest import assert_scaled_close
 from golden_cases import CASE_NAMES, load_case
-from gpu_helpers import announce, coordinates, packed, require_gpu_extension, to_numpy64, upstream
+from gpu_helpers import announce, coordinates, knobs, packed, require_gpu_extension, to_numpy64, upstream
 from oracle import jet, torch_ref
 
 pytestmark = pytest.mark.gpu
@@ -137,6 +137,46 @@ def test_backward_is_bitwise_deterministic_across_runs_grids_and_versions() -> N
         os.environ.pop("FUSED_HOAD_BWD_BLOCKS", None)
         if saved is not None:
             os.environ["FUSED_HOAD_BWD_BLOCKS"] = saved
+
+
+@pytest.mark.parametrize("batch", [1, 17, 1000, 4096, 12288])
+def test_split_backward_agrees_with_the_tiled_kernel(batch: int) -> None:
+    """Up to 768 16-point tiles the backward runs backward_split_kernel (rows split over a
+    workgroup's waves). It does backward_kernel's arithmetic with the sums over points grouped
+    differently, so the two agree to rounding: 1e-5 of each block's scale, ten times tighter
+    than the parity bar."""
+    announce(f"backward split kernel vs tiled kernel, batch={batch}")
+    p = packed(0)
+    x = coordinates(batch, seed=31)
+    gu, gl = upstream(batch, seed=31)
+    with knobs(FUSED_HOAD_BWD_SPLIT="1"):
+        sp, sx = _fused_backward(x, p, gu, gl)
+    with knobs(FUSED_HOAD_BWD_SPLIT="0"):
+        tp, tx = _fused_backward(x, p, gu, gl)
+    for name, lo, hi in BLOCKS:
+        assert_scaled_close(sp[lo:hi], tp[lo:hi], 1e-5, name)
+    assert_scaled_close(sx, tx, 1e-5, "grad_coordinates")
+
+
+def test_split_backward_many_tiles_per_slot_and_saturated_tanh() -> None:
+    announce("backward split kernel forced at batch=20000 (several tiles per slot), weights x3, vs recompute")
+    with knobs(FUSED_HOAD_BWD_SPLIT="1"):
+        (gp, gx), (ep, ex) = _pair(20000, seed=5, scale=3.0)
+    for name, lo, hi in BLOCKS:
+        assert_scaled_close(gp[lo:hi], ep[lo:hi], 1e-4, name)
+    assert_scaled_close(gx, ex, 1e-4, "grad_coordinates")
+
+
+def test_split_backward_is_bitwise_deterministic_across_grids() -> None:
+    announce("backward split kernel determinism: repeats and FUSED_HOAD_BWD_BLOCKS, batch=4096")
+    p = packed(0)
+    x = coordinates(4096, seed=33)
+    gu, gl = upstream(4096, seed=33)
+    ref_p, ref_x = _fused_backward(x, p, gu, gl)
+    for blocks in ("1", "7", "100", "256"):
+        with knobs(FUSED_HOAD_BWD_BLOCKS=blocks):
+            gp, gx = _fused_backward(x, p, gu, gl)
+        assert torch.equal(gp, ref_p) and torch.equal(gx, ref_x), f"changed with {blocks} blocks"
 
 
 def test_backward_handles_empty_batch() -> None:

@@ -8,15 +8,12 @@ max |error| <= 1e-4 max |expected| (test_fused.py:38-49).
 
 from __future__ import annotations
 
-import contextlib
-import os
-
 import numpy as np
 import pytest
 import torch
 
 from golden_cases import CASE_NAMES, load_case
-from gpu_helpers import announce, coordinates, packed, require_gpu_extension, to_numpy64
+from gpu_helpers import announce, coordinates, knobs, packed, require_gpu_extension, to_numpy64
 from oracle import jet, torch_ref
 
 pytestmark = pytest.mark.gpu
@@ -90,21 +87,6 @@ def test_forward_is_bitwise_reproducible_and_version_independent() -> None:
         assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
 
 
-@contextlib.contextmanager
-def _env(**values: str):
-    """Set the kernels' experiment knobs (read per call) for the duration of a block."""
-    saved = {k: os.environ.get(k) for k in values}
-    os.environ.update(values)
-    try:
-        yield
-    finally:
-        for k, v in saved.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
-
-
 @pytest.mark.parametrize("batch", [1000, 65536])
 def test_forward_workgroup_shape_does_not_change_results(batch: int) -> None:
     """12 waves per workgroup (default) and 8 (FUSED_HOAD_FWD_WAVES=8) only distribute tiles
@@ -112,9 +94,9 @@ def test_forward_workgroup_shape_does_not_change_results(batch: int) -> None:
     announce(f"forward 12-wave vs 8-wave workgroups, batch={batch}")
     p = packed(0)
     x = coordinates(batch, seed=17)
-    with _env(FUSED_HOAD_FWD_SPLIT="0"):
+    with knobs(FUSED_HOAD_FWD_SPLIT="0"):
         u12, l12 = _fused(x, p)
-        with _env(FUSED_HOAD_FWD_WAVES="8"):
+        with knobs(FUSED_HOAD_FWD_WAVES="8"):
             u8, l8 = _fused(x, p)
     torch.cuda.synchronize()
     assert torch.equal(u12, u8) and torch.equal(l12, l8)
@@ -132,9 +114,9 @@ def test_split_forward_is_bitwise_equal_to_the_tiled_kernel(batch: int, scale: f
     announce(f"forward split kernel vs tiled kernel, batch={batch}, weights x{scale}")
     p = packed(0) * scale
     x = coordinates(batch, seed=23)
-    with _env(FUSED_HOAD_FWD_SPLIT="0"):
+    with knobs(FUSED_HOAD_FWD_SPLIT="0"):
         u_tiled, l_tiled = _fused(x, p)
-    with _env(FUSED_HOAD_FWD_SPLIT="1"):
+    with knobs(FUSED_HOAD_FWD_SPLIT="1"):
         u_split, l_split = _fused(x, p)
     torch.cuda.synchronize()
     assert torch.equal(u_tiled, u_split) and torch.equal(l_tiled, l_split)

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from conftest import assert_scaled_close
-from gpu_helpers import announce, coordinates, require_gpu_extension, to_numpy64
+from gpu_helpers import announce, coordinates, knobs, require_gpu_extension, to_numpy64
 
 pytestmark = pytest.mark.gpu
 
@@ -337,3 +337,25 @@ def test_pinn_step_is_bitwise_deterministic_and_grid_independent() -> None:
         del os.environ["FUSED_HOAD_BWD_BLOCKS"]
     for a, b, c in zip(first, second, capped):
         assert torch.equal(a, b) and torch.equal(a, c)
+
+
+@pytest.mark.parametrize("batch,nb", [(1000, 100), (4096, 0), (12000, 288)])
+def test_split_gradient_kernel_agrees_with_the_tiled_one(batch: int, nb: int) -> None:
+    """Small batches run backward_split_kernel; forced either way, the two gradient kernels
+    give the same loss and gradient up to rounding (1e-5 of each block's scale)."""
+    announce(f"fused step, split vs tiled gradient kernel, batch={batch}, boundary={nb}")
+    from fused_hoad.training import FusedPoissonAdam
+
+    x = coordinates(batch, seed=17)
+    xb = _boundary(nb, 17) if nb else None
+    results = []
+    for split in ("1", "0"):
+        trainer = FusedPoissonAdam(_model(3), x, boundary=xb)
+        with knobs(FUSED_HOAD_BWD_SPLIT=split):
+            loss = trainer.step()
+        torch.cuda.synchronize()
+        results.append((float(loss), to_numpy64(trainer.grad)))
+    (loss_s, grad_s), (loss_t, grad_t) = results
+    assert loss_s == pytest.approx(loss_t, rel=1e-6)
+    for name, start, end in _blocks():
+        assert_scaled_close(grad_s[start:end], grad_t[start:end], 1e-5, name)
