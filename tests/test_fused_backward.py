@@ -158,6 +158,17 @@ def test_split_backward_agrees_with_the_tiled_kernel(batch: int) -> None:
     assert_scaled_close(sx, tx, 1e-5, "grad_coordinates")
 
 
+@pytest.mark.parametrize("batch", [12288, 12289])
+def test_backward_on_both_sides_of_the_kernel_threshold(batch: int) -> None:
+    """12,288 points (768 16-point tiles) still run backward_split_kernel, 12,289 run
+    backward_kernel; both meet the parity bar against the recompute backward."""
+    announce(f"backward at the split-kernel threshold, batch={batch}, vs recompute")
+    (gp, gx), (ep, ex) = _pair(batch, seed=8)
+    for name, lo, hi in BLOCKS:
+        assert_scaled_close(gp[lo:hi], ep[lo:hi], 1e-4, name)
+    assert_scaled_close(gx, ex, 1e-4, "grad_coordinates")
+
+
 def test_split_backward_many_tiles_per_slot_and_saturated_tanh() -> None:
     announce("backward split kernel forced at batch=20000 (several tiles per slot), weights x3, vs recompute")
     with knobs(FUSED_HOAD_BWD_SPLIT="1"):

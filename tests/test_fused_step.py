@@ -264,7 +264,10 @@ def _boundary(count: int, seed: int):
     return boundary_points(count, device="cpu", generator=torch.Generator().manual_seed(seed)).cuda()
 
 
-@pytest.mark.parametrize("batch,nb", [(1000, 100), (100, 1), (100, 63), (64, 64), (100, 65), (20000, 1024)])
+@pytest.mark.parametrize(
+    "batch,nb",
+    [(1000, 100), (100, 1), (100, 63), (64, 64), (100, 65), (12000, 288), (12000, 289), (20000, 1024)],
+)
 def test_pinn_step_with_boundary_matches_the_oracle(batch: int, nb: int) -> None:
     announce(f"fused PINN+Adam step (boundary term) vs float64 oracle, batch={batch}, boundary={nb}")
     from oracle import adam
