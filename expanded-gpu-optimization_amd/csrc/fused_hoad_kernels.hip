@@ -321,14 +321,23 @@ __device__ __forceinline__ void hidden_product(const float* w, const f4 (&h)[4][
 }
 
 // Forward hidden product with the operand-native weight layout: wa points at this lane's f4
-// in the layer's block; k-step (ob, j) reads wa[(4 ob + j) * 64].
+// in the layer's block; k-step (ob, j) reads wa[(4 ob + j) * 64]. Each k-step's operand is
+// read one k-step ahead, with a fence on both sides of the step's 16 MFMAs so the read stays
+// there: a wave that runs alone on its SIMD (the last tiles of a launch) then waits for no LDS
+// read; left alone, the compiler issued each read right before its MFMAs. `first` = wa[0],
+// read by the caller before the previous layer's tanh jet.
 __device__ __forceinline__ void hidden_product_native(const f4* wa, const f4 (&h)[4][4],
-                                                      const f4 (&bias)[4], f4 (&acc)[4][4]) {
+                                                      const f4 (&bias)[4], f4 (&acc)[4][4],
+                                                      f4 first) {
+  f4 next = first;
 #pragma unroll
   for (int ob = 0; ob < 4; ++ob) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const f4 a = wa[(4 * ob + j) * kWave];
+      const int step = 4 * ob + j;
+      const f4 a = next;
+      if (step < 15) next = wa[(step + 1) * kWave];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -337,6 +346,7 @@ __device__ __forceinline__ void hidden_product_native(const f4* wa, const f4 (&h
           acc[mb][c] = mfma(a[mb], h[ob][c][j], cin);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -510,36 +520,52 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
                int64_t tiles) {
   __shared__ __attribute__((aligned(16))) float s_wa[3 * kOperandLayerF4 * 4];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
-  stage_operand_weights<kWaves * kWave>(params, s_wa, threadIdx.x);
-  stage_small(params, s_small, threadIdx.x, kWaves * kWave);
-  __syncthreads();
-
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int g = lane >> 4;
-  const f4* wa_lane = reinterpret_cast<const f4*>(s_wa) + lane;
-  const int64_t step = static_cast<int64_t>(gridDim.x) * kWaves;
   const int m = lane & 15;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kWaves;
+  // Coordinates are read one tile ahead (the first tile's during the staging), so no tile
+  // waits for global memory; a wave that runs alone on its SIMD would expose that latency.
+  int64_t tile = blockIdx.x + static_cast<int64_t>(wave) * gridDim.x;
+  float next_x0 = 0.0f, next_x1 = 0.0f;
+  if (tile * kTile + m < batch) {
+    next_x0 = coordinates[2 * (tile * kTile + m)];
+    next_x1 = coordinates[2 * (tile * kTile + m) + 1];
+  }
+  stage_operand_weights<kWaves * kWave>(params, s_wa, threadIdx.x);
+  stage_small(params, s_small, threadIdx.x, kWaves * kWave);
+  __syncthreads();
+  next_x0 = opaque(next_x0);  // delivered before the loop, for the same reason as below
+  next_x1 = opaque(next_x1);
 
-  for (int64_t tile = blockIdx.x + static_cast<int64_t>(wave) * gridDim.x; tile < tiles;
-       tile += step) {
+  const f4* wa_lane = reinterpret_cast<const f4*>(s_wa) + lane;
+  for (; tile < tiles; tile += step) {
     keep_lds_reads_in_loop();
     const int64_t point = tile * kTile + m;
     const bool active = point < batch;
-    float x0 = 0.0f, x1 = 0.0f;
-    if (active) {
-      x0 = coordinates[2 * point];
-      x1 = coordinates[2 * point + 1];
+    const float x0 = next_x0, x1 = next_x1;
+    const int64_t next_point = (tile + step) * kTile + m;
+    if (next_point < batch) {
+      next_x0 = coordinates[2 * next_point];
+      next_x1 = coordinates[2 * next_point + 1];
     }
+    f4 first = wa_lane[0];
     f4 h[4][4];
     layer0_forward(s_small, g, x0, x1, h);
     for (int layer = 0; layer < 3; ++layer) {
       f4 bias[4];
       load_bias(s_small, layer, g, bias);
       f4 acc[4][4];
-      hidden_product_native(wa_lane + layer * kOperandLayerF4, h, bias, acc);
+      hidden_product_native(wa_lane + layer * kOperandLayerF4, h, bias, acc, first);
+      if (layer < 2) first = wa_lane[(layer + 1) * kOperandLayerF4];
       apply_tanh_jet(acc, h);
     }
+    // Take delivery of the next coordinates here, before this tile's stores: a wait at the
+    // top of the next tile would also wait for those stores (they sit behind a branch, so the
+    // compiler cannot count them), and a store takes far longer than a tile's head.
+    next_x0 = opaque(next_x0);
+    next_x1 = opaque(next_x1);
     // u = w_out . v + b_out and lap = w_out . L, from the scaled jet.
     float u = 0.0f, lap = 0.0f;
 #pragma unroll
