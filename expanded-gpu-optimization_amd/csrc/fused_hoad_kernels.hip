@@ -1117,6 +1117,50 @@ __device__ __forceinline__ void boundary_value_tile(const float* s_w, const floa
   }
 }
 
+// Per-point inputs of one gradient-kernel tile for this lane: coordinates and, for interior
+// points, the upstream gradients (gu, gl) or, with kLoss, the source f (in a). Boundary tiles
+// (kLoss, tile >= seed.interior_tiles) take boundary coordinates. Inactive lanes get zeros.
+struct TileInputs {
+  float x0, x1, a, b;
+};
+
+template <bool kLoss>
+__device__ __forceinline__ TileInputs load_tile_inputs(const float* __restrict__ coordinates,
+                                                       const float* __restrict__ grad_output,
+                                                       const float* __restrict__ grad_laplacian,
+                                                       int64_t batch, const LossSeed& seed,
+                                                       int64_t tile, int w, int m) {
+  TileInputs in{0.f, 0.f, 0.f, 0.f};
+  if (kLoss && tile >= seed.interior_tiles) {
+    const int64_t point = (tile - seed.interior_tiles) * kBwdTile + kTile * w + m;
+    if (point < seed.boundary_count) {
+      in.x0 = seed.boundary[2 * point];
+      in.x1 = seed.boundary[2 * point + 1];
+    }
+    return in;
+  }
+  const int64_t point = tile * kBwdTile + kTile * w + m;
+  if (point < batch) {
+    in.x0 = coordinates[2 * point];
+    in.x1 = coordinates[2 * point + 1];
+    if (kLoss) {
+      in.a = seed.source[point];
+    } else {
+      in.a = grad_output[point];
+      in.b = grad_laplacian[point];
+    }
+  }
+  return in;
+}
+
+// Force delivery of prefetched inputs at this point (an opaque use of each register).
+__device__ __forceinline__ void deliver(TileInputs& in) {
+  in.x0 = opaque(in.x0);
+  in.x1 = opaque(in.x1);
+  in.a = opaque(in.a);
+  in.b = opaque(in.b);
+}
+
 // z of hidden layers 2 and 3 stays in registers through the walk back; z of hidden layer 1
 // would push the live state past the register file, so each wave parks it in its own 16 KB
 // of the workspace (`stash`, coalesced 16-byte stores, L2-resident) and reloads it after
@@ -1135,13 +1179,19 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   __shared__ __attribute__((aligned(16))) float s_stage[4 * kPlane];
   __shared__ float s_red[3][kBwdWaves];
   if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] += 1.0f;
-  stage_parameters<kBwdWaves * kWave>(params, s_w, s_small, threadIdx.x);
-  __syncthreads();
-
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int m = lane & 15;
   const int g = lane >> 4;
+  // The first slot's first tile inputs are read before the staging, which hides their latency.
+  TileInputs next{0.f, 0.f, 0.f, 0.f};
+  if (static_cast<int>(blockIdx.x) < slots) {
+    next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed,
+                                   blockIdx.x, w, m);
+  }
+  stage_parameters<kBwdWaves * kWave>(params, s_w, s_small, threadIdx.x);
+  __syncthreads();
+
   // Lane offsets into the LDS arrays. Each use forms its base from an opaque copy: the arrays
   // span more than the 64 KB reach of a DS offset, and hoisted bases would be spilled.
   const int rows_off = lane_rows(m, g);
@@ -1162,34 +1212,36 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     }
     acc.w0x = acc.w0y = acc.b0 = acc.wout = acc.bout = acc.loss = acc.bloss = 0.f;
 
+    // Per-point inputs are read one tile ahead and delivered mid-tile (deliver), so no tile
+    // starts with a wait on global memory: with one wave per SIMD nothing would hide it. The
+    // delivery sits before the tile's own stores, which a wait at the next tile's head would
+    // also have to wait for (they are behind branches, so the compiler cannot count them).
+    if (slot != static_cast<int>(blockIdx.x)) {
+      next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed, slot,
+                                     w, m);
+    }
+    deliver(next);
     for (int64_t tile = slot; tile < tiles; tile += slots) {
       keep_lds_reads_in_loop();
       const int m_pick = opaque(m);  // pick_row_sum's 16 lane masks stay inside the tile
+      const TileInputs in = next;
+      if (tile + slots < tiles) {
+        next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed,
+                                       tile + slots, w, m);
+      }
+      const float x0 = in.x0, x1 = in.x1;
       if (kLoss && tile >= seed.interior_tiles) {  // boundary tile (uniform per workgroup)
         const int64_t point = (tile - seed.interior_tiles) * kBwdTile + kTile * w + m;
         const bool active = point < seed.boundary_count;
-        float x0 = 0.f, x1 = 0.f;
-        if (active) {
-          x0 = seed.boundary[2 * point];
-          x1 = seed.boundary[2 * point + 1];
-        }
         boundary_value_tile(s_w, s_small, s_stage, rows_off, cols_off, stage_lane_off, w, g,
                             m_pick, x0, x1, active, seed.boundary_scale, acc);
+        deliver(next);
         continue;
       }
       const int64_t point = tile * kBwdTile + kTile * w + m;
       const bool active = point < batch;
-      float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f, f = 0.f;
-      if (active) {
-        x0 = coordinates[2 * point];
-        x1 = coordinates[2 * point + 1];
-        if (kLoss) {
-          f = seed.source[point];
-        } else {
-          gu = grad_output[point];
-          gl = grad_laplacian[point];
-        }
-      }
+      float gu = kLoss ? 0.f : in.a, gl = kLoss ? 0.f : in.b;
+      const float f = kLoss ? in.a : 0.f;
 
       // ---- 1. forward recompute ----
       f4 h[4][4];
@@ -1275,6 +1327,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       stage_and_dw<false>(z2, z1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
                           s_stage + opaque(rows_off), s_small, w, g, x0, x1,
                           tv, ts);
+      deliver(next);  // the stash reload above has been waited for, and so has this
       hidden_product_t(s_w + opaque(cols_off) + kPlane, z2, hb);
 
       // ---- 5. hidden layer 1 ----
