@@ -46,6 +46,9 @@ FLOP_PER_POINT_BACKWARD = 2 * FLOP_PER_POINT_FORWARD  # dW + hbar (recompute not
 REFERENCE_A5000 = {"residual_points_per_s_64k": 121.9e6, "train_step_ms_64k": 3.334,
                    "hardware": "RTX A5000", "source": "reference results/2026-11-06-RTX-A5000-8454035"}
 TRAFFIC_FILE = ROOT / "profiles" / "forward_kernel_65536_traffic.json"
+CPU_RESIDUAL_CALLS = 200     # CPU baseline sample sizes (see _cpu_baseline)
+CPU_RESIDUAL_1K_CALLS = 200
+CPU_STEP_CALLS = 40
 
 
 def log(message: str) -> None:
@@ -389,12 +392,14 @@ def _cpu_baseline(torch) -> dict:
             samples.append((time.perf_counter() - tick) * 1e3)
         return statistics.median(samples)
 
+    # About 10 s of CPU work in all (the 64K residual about 5 s, the eager step about 5 s on a
+    # 16-thread host), so that the medians are stable and the bench still ends within minutes.
     with torch.no_grad():
-        res64k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x), 1, 5)
-        res1k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x1k), 3, 20)
+        res64k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x), 2, CPU_RESIDUAL_CALLS)
+        res1k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x1k), 5, CPU_RESIDUAL_1K_CALLS)
     optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)
     source = torch_ref.poisson_source(x)
-    step_ms = median_ms(lambda: torch_ref.eager_train_step(model, x, source, optimizer), 1, 3)
+    step_ms = median_ms(lambda: torch_ref.eager_train_step(model, x, source, optimizer), 2, CPU_STEP_CALLS)
     cpu_model = "?"
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -410,9 +415,10 @@ def _cpu_baseline(torch) -> dict:
         "unit": "points/s",
         "cores": threads,
         "kind": "port",
-        "sample": "oracle/torch_ref.py PyTorch forward Laplacian (u, Lap u) at 65,536 points, median of 5 calls "
-                  f"after 1 warmup ({res64k_ms:.1f} ms/call); 1,024 points: {res1k_ms:.2f} ms/call (median of 20); "
-                  f"eager nested-autograd + Adam train step at 65,536 points: {step_ms:.1f} ms/step (median of 3)",
+        "sample": f"oracle/torch_ref.py PyTorch forward Laplacian (u, Lap u) at 65,536 points, median of "
+                  f"{CPU_RESIDUAL_CALLS} calls after 2 warmup ({res64k_ms:.1f} ms/call); 1,024 points: "
+                  f"{res1k_ms:.2f} ms/call (median of {CPU_RESIDUAL_1K_CALLS}); eager nested-autograd + Adam "
+                  f"train step at 65,536 points: {step_ms:.1f} ms/step (median of {CPU_STEP_CALLS})",
         "train_step_ms": round(step_ms, 3),
         "residual_1k_ms": round(res1k_ms, 4),
         "os_cpu_count": os.cpu_count(),
