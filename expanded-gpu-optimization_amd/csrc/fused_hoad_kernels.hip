@@ -142,6 +142,44 @@ __device__ __forceinline__ void tanh_jet_adjoint_vs(float v, float s, float zj0,
   bl = s * bl;
 }
 
+// tanh_jet_adjoint_vs for the output layer's seed, whose Jbar is zero (the output feeds only
+// u and the Laplacian), and with kZeroV also vbar = 0 (interior points of the fused step: the
+// loss has no u term there). It drops only operations on those zeros, so its results are the
+// general form's, up to the sign of an exact zero.
+template <bool kZeroV>
+__device__ __forceinline__ void tanh_jet_adjoint_seed(float v, float s, float zj0, float zj1,
+                                                      float zl, float& bv, float& bj0,
+                                                      float& bj1, float& bl) {
+  const float q = __builtin_fmaf(zj0, zj0, zj1 * zj1);
+  const float p = __builtin_fmaf(v, q, zl);
+  const float kv = kKappa * v;
+  const float t2 = __builtin_fmaf(kv, p, s * q);
+  const float nv = kZeroV ? s * (bl * t2) : s * __builtin_fmaf(bl, t2, bv);
+  const float lbv = 2.0f * bl * v;
+  bj0 = s * (lbv * zj0);
+  bj1 = s * (lbv * zj1);
+  bv = nv;
+  bl = s * bl;
+}
+
+// tanh_jet_adjoint_vs for layer 0, whose z_J are the W0 columns and z_L = 0: q = |z_J|^2 is
+// the per-neuron constant staged in kSmallQ0 (the same fma), and p = v q.
+__device__ __forceinline__ void tanh_jet_adjoint_layer0(float v, float s, float zj0, float zj1,
+                                                        float q, float& bv, float& bj0,
+                                                        float& bj1, float& bl) {
+  const float dot = __builtin_fmaf(bj0, zj0, bj1 * zj1);
+  const float p = v * q;
+  const float kv = kKappa * v;
+  const float t1 = __builtin_fmaf(kv, dot, bv);
+  const float t2 = __builtin_fmaf(kv, p, s * q);
+  const float nv = s * __builtin_fmaf(bl, t2, t1);
+  const float lbv = 2.0f * bl * v;
+  bj0 = s * __builtin_fmaf(lbv, zj0, bj0);
+  bj1 = s * __builtin_fmaf(lbv, zj1, bj1);
+  bv = nv;
+  bl = s * bl;
+}
+
 // Small-parameter staging shared by both kernels (see kSmallCwx for the scaled forms).
 __device__ __forceinline__ void stage_small(const float* __restrict__ params, float* s_small,
                                             int tid, int threads) {
@@ -508,6 +546,45 @@ __device__ __forceinline__ float sum_row16(float x) {
   return x;
 }
 
+template <int kCtrl>
+__device__ __forceinline__ float dpp_read(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, true));
+}
+
+// Reduce-scatter over the 16 lanes of a row: lane m of the row (m = lane % 16) returns the sum
+// of v[m] over the row's lanes. Four butterfly stages, with partners given by DPP: the row
+// mirror (lane 15 - m), the half-row mirror (7 - m within each 8), then quad xor 2 and xor 1.
+// At each stage a lane keeps the half of its partial sums whose indices it or its remaining
+// partners will own and adds the partner's copy of that half, so the work halves per stage:
+// 45 VALU instructions, against 80 for 16 full row sums and picks.
+__device__ __forceinline__ float row_reduce_scatter16(const float (&v)[16], int m) {
+  const bool b3 = (m & 8) != 0, b2 = (m & 4) != 0, b1 = (m & 2) != 0, b0 = (m & 1) != 0;
+  float s8[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float keep = b3 ? v[j + 8] : v[j];
+    const float send = b3 ? v[j] : v[j + 8];
+    s8[j] = keep + dpp_read<0x140>(send);
+  }
+  float s4[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float keep = b2 ? s8[k + 4] : s8[k];
+    const float send = b2 ? s8[k] : s8[k + 4];
+    s4[k] = keep + dpp_read<0x141>(send);
+  }
+  float s2[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float keep = b1 ? s4[k + 2] : s4[k];
+    const float send = b1 ? s4[k] : s4[k + 2];
+    s2[k] = keep + dpp_read<0x4E>(send);
+  }
+  const float keep = b0 ? s2[1] : s2[0];
+  const float send = b0 ? s2[0] : s2[1];
+  return keep + dpp_read<0xB1>(send);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Forward kernel (replaces fused_forward_laplacian_tiled_kernel<2>,
 // /root/reference/csrc/fused_residual.cu:157-295). A grid of at most one workgroup per CU
@@ -718,7 +795,7 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
 //   3. dW contracts over the points of all 4 waves: zbar and h_prev are staged in LDS (two
 //      components at a time) and wave w owns output rows 16 w .. 16 w + 15 of every dW; the
 //      hidden bias gradients fall out of the same LDS reads. W0, b0 and w_out gradients are
-//      summed over each wave's points in registers (pick_row_sum) and over the 4 waves once
+//      summed over each wave's points in registers (row_reduce_scatter16) and over the 4 waves once
 //      per slot.
 // Weight gradients accumulate in registers across the tiles of a "slot": slot s takes the
 // workgroup tiles s, s + slots, s + 2 slots, ... in that order and writes one partial row.
@@ -774,14 +851,30 @@ __device__ __forceinline__ float dw_product(const float* stage_rows, int w, f4 (
 }
 
 // Per-neuron sums over a wave's 16 points without LDS: lane (m, g) holds x for neuron
-// 16 mb + 4 g + r at point m, so a DPP row sum gives that neuron's total in all 16 lanes of row
-// g. Lane (m, g) keeps the total of neuron owned_neuron(m, g) = 16 (m >> 2) + 4 g + (m & 3):
-// the 64 lanes own the 64 neurons once each.
+// 16 mb + 4 g + r at point m, so summing value k = 4 mb + r over the 16 lanes of row g gives
+// that neuron's total; row_reduce_scatter16 leaves the total of k = m in lane m. Lane (m, g)
+// thus keeps the total of neuron owned_neuron(m, g) = 16 (m >> 2) + 4 g + (m & 3): the 64 lanes
+// own the 64 neurons once each.
 __device__ __forceinline__ int owned_neuron(int m, int g) { return 16 * (m >> 2) + 4 * g + (m & 3); }
 
-__device__ __forceinline__ void pick_row_sum(float x, int k, int m, float& keep) {
-  const float total = sum_row16(x);
-  keep = (m == k) ? total : keep;
+// hidden layer 3's tanh_adjoint_in_place, from the output layer's seed (Jbar = 0, and with
+// kZeroV vbar = 0): tanh_jet_adjoint_seed.
+template <bool kZeroV>
+__device__ __forceinline__ void tanh_adjoint_seed_in_place(f4 (&z)[4][4], const f4 (&hb)[4][4],
+                                                           const f4 (&tv)[4], const f4 (&ts)[4]) {
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float bv = hb[mb][0][r], bj0 = 0.0f, bj1 = 0.0f, bl = hb[mb][3][r];
+      tanh_jet_adjoint_seed<kZeroV>(tv[mb][r], ts[mb][r], z[mb][1][r], z[mb][2][r], z[mb][3][r],
+                                    bv, bj0, bj1, bl);
+      z[mb][0][r] = bv;
+      z[mb][1][r] = bj0;
+      z[mb][2][r] = bj1;
+      z[mb][3][r] = bl;
+    }
+  }
 }
 
 // Replace a hidden layer's pre-activation z by its adjoint zbar, given the adjoint hb of the
@@ -1068,17 +1161,17 @@ __device__ __forceinline__ void boundary_value_tile(const float* s_w, const floa
   const float gu_c = gu * (1.0f / kC);
   f4 zb[4], hb[4];
   {
-    float wout_sum = 0.0f;
+    float wout_terms[16];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
       const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pick_row_sum(gu_c * tv[mb][r], 4 * mb + r, m_pick, wout_sum);
+        wout_terms[4 * mb + r] = gu_c * tv[mb][r];
         zb[mb][r] = ts[mb][r] * (gu * wv[r]);  // hidden layer 3's zbar_v = s vbar
       }
     }
-    acc.wout += wout_sum;
+    acc.wout += row_reduce_scatter16(wout_terms, m_pick);
     acc.bout += sum_row16(gu);
   }
 
@@ -1099,21 +1192,21 @@ __device__ __forceinline__ void boundary_value_tile(const float* s_w, const floa
 
   // Layer 0: bv = s hbar_v; dW0[o][d] = sum_p bv (c x_d), db0 = c sum_p bv.
   {
-    float w0x_sum = 0.f, w0y_sum = 0.f, b0_sum = 0.f;
+    float tx[16], ty[16], tb[16];
     const float cx0 = kC * x0, cx1 = kC * x1;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float bv = ts[mb][r] * hb[mb][r];
-        pick_row_sum(bv * cx0, 4 * mb + r, m_pick, w0x_sum);
-        pick_row_sum(bv * cx1, 4 * mb + r, m_pick, w0y_sum);
-        pick_row_sum(bv, 4 * mb + r, m_pick, b0_sum);
+        tx[4 * mb + r] = bv * cx0;
+        ty[4 * mb + r] = bv * cx1;
+        tb[4 * mb + r] = bv;
       }
     }
-    acc.w0x += w0x_sum;
-    acc.w0y += w0y_sum;
-    acc.b0 += b0_sum;
+    acc.w0x += row_reduce_scatter16(tx, m_pick);
+    acc.w0y += row_reduce_scatter16(ty, m_pick);
+    acc.b0 += row_reduce_scatter16(tb, m_pick);
   }
 }
 
@@ -1223,7 +1316,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     deliver(next);
     for (int64_t tile = slot; tile < tiles; tile += slots) {
       keep_lds_reads_in_loop();
-      const int m_pick = opaque(m);  // pick_row_sum's 16 lane masks stay inside the tile
+      const int m_pick = opaque(m);  // row_reduce_scatter16's lane masks stay inside the tile
       const TileInputs in = next;
       if (tile + slots < tiles) {
         next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed,
@@ -1283,32 +1376,34 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       // ---- 2. output layer: w_out / b_out gradients and the adjoint seed ----
       // In the scaled jet u = (w_out / c) . v' and lap = (w_out / lambda) . L', so
       // dw_out = sum_p (gu / c) v' + (gl / lambda) L' and the seeds are vbar' = gu w_out / c,
-      // Lbar' = gl w_out / lambda, Jbar = 0. The point sums stay in registers (pick_row_sum).
+      // Lbar' = gl w_out / lambda, Jbar = 0. The point sums stay in registers (row_reduce_scatter16).
+      // With kLoss, gu = 0 on interior points: the value seed and the u terms are dropped
+      // (their products with zero), which leaves the other results as they were.
       f4 hb[4][4];
       {
         const float gu_c = gu * (1.0f / kC);
         const float gl_l = gl * (1.0f / kLambda);
-        float wout_sum = 0.0f;
+        float wout_terms[16];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
           const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
           const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            pick_row_sum(__builtin_fmaf(gu_c, h[mb][0][r], gl_l * h[mb][3][r]), 4 * mb + r, m_pick,
-                         wout_sum);
-            hb[mb][0][r] = gu * wv[r];
+            wout_terms[4 * mb + r] = kLoss ? gl_l * h[mb][3][r]
+                                           : __builtin_fmaf(gu_c, h[mb][0][r], gl_l * h[mb][3][r]);
+            hb[mb][0][r] = kLoss ? 0.0f : gu * wv[r];
             hb[mb][1][r] = 0.0f;
             hb[mb][2][r] = 0.0f;
             hb[mb][3][r] = gl * wl[r];
           }
         }
-        acc.wout += wout_sum;
-        acc.bout += sum_row16(gu);
+        acc.wout += row_reduce_scatter16(wout_terms, m_pick);
+        if (!kLoss) acc.bout += sum_row16(gu);
       }
 
       // ---- 3. hidden layer 3 ----
-      tanh_adjoint_in_place(z3, hb, tv, ts);
+      tanh_adjoint_seed_in_place<kLoss>(z3, hb, tv, ts);
       stage_and_dw<false>(z3, z2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
                           s_stage + opaque(rows_off), s_small, w, g, x0, x1,
                           tv, ts);
@@ -1341,7 +1436,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       // bv is the adjoint of c z_v, so zbar_v = c bv: grad_x = (c W0)^T bv,
       // dW0[o][d] = sum_p bv (c x_d) + zbar_Jd, db0 = c sum_p bv.
       {
-        float gx0 = 0.f, gx1 = 0.f, w0x_sum = 0.f, w0y_sum = 0.f, b0_sum = 0.f;
+        float gx0 = 0.f, gx1 = 0.f, tx[16], ty[16], tb[16];
         const float cx0 = kC * x0, cx1 = kC * x1;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
@@ -1349,17 +1444,18 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             float bv = hb[mb][0][r], bj0 = hb[mb][1][r], bj1 = hb[mb][2][r], bl = hb[mb][3][r];
-            tanh_jet_adjoint_vs(tv[mb][r], ts[mb][r], w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
+            tanh_jet_adjoint_layer0(tv[mb][r], ts[mb][r], w0.wx[r], w0.wy[r], w0.q[r], bv, bj0,
+                                    bj1, bl);
             gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
             gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
-            pick_row_sum(__builtin_fmaf(bv, cx0, bj0), 4 * mb + r, m_pick, w0x_sum);  // dW0[o][0]
-            pick_row_sum(__builtin_fmaf(bv, cx1, bj1), 4 * mb + r, m_pick, w0y_sum);  // dW0[o][1]
-            pick_row_sum(bv, 4 * mb + r, m_pick, b0_sum);                              // db0[o] / c
+            tx[4 * mb + r] = __builtin_fmaf(bv, cx0, bj0);  // dW0[o][0]
+            ty[4 * mb + r] = __builtin_fmaf(bv, cx1, bj1);  // dW0[o][1]
+            tb[4 * mb + r] = bv;                            // db0[o] / c
           }
         }
-        acc.w0x += w0x_sum;
-        acc.w0y += w0y_sum;
-        acc.b0 += b0_sum;
+        acc.w0x += row_reduce_scatter16(tx, m_pick);
+        acc.w0y += row_reduce_scatter16(ty, m_pick);
+        acc.b0 += row_reduce_scatter16(tb, m_pick);
         gx0 = sum_lane_groups(gx0);
         gx1 = sum_lane_groups(gx1);
         if (g == 0 && active && (!kLoss || grad_coordinates != nullptr)) {
