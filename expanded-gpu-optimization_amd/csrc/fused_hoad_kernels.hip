@@ -1897,6 +1897,15 @@ reduce_adam_kernel(const float* __restrict__ partials, int slots, AdamArgs a) {
   const int col = threadIdx.x & 63;
   const int group = threadIdx.x >> 6;
   const int k = blockIdx.x * 64 + col;
+  // The Adam state is read before the partial rows, so the two memory round trips overlap.
+  const bool updates = group == 0 && k < kParameterCount;
+  float p = 0.0f, m = 0.0f, v = 0.0f;
+  if (updates) {
+    p = a.params[k];
+    m = a.exp_avg[k];
+    v = a.exp_avg_sq[k];
+  }
+  const float step_count = a.step[0];
   const float total = fixed_tree_sum(partials, slots, k, kLossColumn + 2, s_part, group, col);
   if (group == 0 && (k == kLossColumn || k == kLossColumn + 1)) s_loss[k - kLossColumn] = total;
   __syncthreads();
@@ -1907,9 +1916,9 @@ reduce_adam_kernel(const float* __restrict__ partials, int slots, AdamArgs a) {
                                        : interior;
     return;
   }
-  if (k >= kParameterCount) return;
+  if (!updates) return;
   if (a.grad) a.grad[k] = total;
-  const double t = static_cast<double>(a.step[0]);
+  const double t = static_cast<double>(step_count);
   const double bc1 = 1.0 - pow(a.beta1, t);
   const double bc2 = 1.0 - pow(a.beta2, t);
   const float step_size = static_cast<float>(-(a.lr / bc1));
@@ -1920,12 +1929,10 @@ reduce_adam_kernel(const float* __restrict__ partials, int slots, AdamArgs a) {
   const float eps = static_cast<float>(a.eps);
   const float wd = static_cast<float>(a.weight_decay);
 
-  float p = a.params[k];
   float g = total;
   if (wd != 0.0f) g = g + wd * p;
-  float m = a.exp_avg[k];
   m = m + w1 * (g - m);  // lerp with weight < 0.5
-  float v = a.exp_avg_sq[k] * b2;
+  v = v * b2;
   v = v + w2 * g * g;
   const float denom = sqrtf(v) / bc2_sqrt + eps;
   p = p + step_size * m / denom;
