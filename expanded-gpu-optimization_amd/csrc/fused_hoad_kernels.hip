@@ -105,6 +105,27 @@ __device__ __forceinline__ void tanh_scaled(float zv, float& v, float& s) {
   v = __builtin_copysignf(__builtin_fmaf(w, -kAbsC, kAbsC), zv);
 }
 
+// tanh_scaled of four values, in stages across the four: the four exp2, then the four rcp, then
+// the rest, with fences so the scheduler keeps the stages. Each value's chain is serial
+// (exp2 -> fma -> rcp -> mul), and left alone the compiler ran the chains one after another
+// with two temporaries; a wave alone on its SIMD (the backward, the forward's last tiles) then
+// waited out every transcendental's latency. Same operations per value as tanh_scaled.
+__device__ __forceinline__ void tanh_scaled4(const f4 zv, f4& v, f4& s) {
+  f4 t, u;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) t[r] = __builtin_amdgcn_exp2f(-__builtin_fabsf(zv[r]));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) u[r] = __builtin_amdgcn_rcpf(__builtin_fmaf(t[r], 0.5f, 0.5f));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float w = t[r] * u[r];
+    s[r] = u[r] * w;
+    v[r] = __builtin_copysignf(__builtin_fmaf(w, -kAbsC, kAbsC), zv[r]);
+  }
+}
+
 // Forward tanh jet in scaled variables: (c z_v, z_J0, z_J1, lambda z_L) ->
 // (c v, J0, J1, lambda L) with v = tanh z_v, J = s z_J, L = s z_L - 2 v s q, q = |z_J|^2.
 __device__ __forceinline__ void tanh_jet(float zv, float zj0, float zj1, float zl, float& v,
@@ -437,17 +458,20 @@ __device__ __forceinline__ void hidden_layer(const float* s_small, const float* 
   hidden_product(w_rows + layer * kPlane, h, bias, acc);
 }
 
+// tanh_jet over a layer's 16 values per lane, the tanh four at a time (tanh_scaled4).
 __device__ __forceinline__ void apply_tanh_jet(const f4 (&z)[4][4], f4 (&h)[4][4]) {
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
+    f4 v, sl;
+    tanh_scaled4(z[mb][0], v, sl);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float v, j0, j1, l;
-      tanh_jet(z[mb][0][r], z[mb][1][r], z[mb][2][r], z[mb][3][r], v, j0, j1, l);
-      h[mb][0][r] = v;
-      h[mb][1][r] = j0;
-      h[mb][2][r] = j1;
-      h[mb][3][r] = l;
+      const float zj0 = z[mb][1][r], zj1 = z[mb][2][r];
+      const float q = __builtin_fmaf(zj0, zj0, zj1 * zj1);
+      h[mb][0][r] = v[r];
+      h[mb][1][r] = sl[r] * zj0;
+      h[mb][2][r] = sl[r] * zj1;
+      h[mb][3][r] = sl[r] * __builtin_fmaf(v[r], q, z[mb][3][r]);
     }
   }
 }
@@ -457,10 +481,11 @@ __device__ __forceinline__ void apply_tanh_jet_vs(const f4 (&z)[4][4], f4 (&h)[4
                                                   f4 (&tv)[4], f4 (&ts)[4]) {
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
+    f4 v4, s4;
+    tanh_scaled4(z[mb][0], v4, s4);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float v, sl;
-      tanh_scaled(z[mb][0][r], v, sl);
+      const float v = v4[r], sl = s4[r];
       const float q = __builtin_fmaf(z[mb][1][r], z[mb][1][r], z[mb][2][r] * z[mb][2][r]);
       h[mb][0][r] = v;
       h[mb][1][r] = sl * z[mb][1][r];
@@ -478,14 +503,16 @@ __device__ __forceinline__ void apply_tanh_jet_vs(const f4 (&z)[4][4], f4 (&h)[4
 __device__ __forceinline__ void layer0_block(const float* s_small, int mb, int g, float x0,
                                              float x1, f4 (&h)[4]) {
   const Layer0Weights w = layer0_weights(s_small, mb, g);
+  f4 zv, v, s;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) zv[r] = layer0_zv(w, r, x0, x1);
+  tanh_scaled4(zv, v, s);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    float v, s;
-    tanh_scaled(layer0_zv(w, r, x0, x1), v, s);
-    h[0][r] = v;
-    h[1][r] = s * w.wx[r];
-    h[2][r] = s * w.wy[r];
-    h[3][r] = s * (v * w.q[r]);
+    h[0][r] = v[r];
+    h[1][r] = s[r] * w.wx[r];
+    h[2][r] = s[r] * w.wy[r];
+    h[3][r] = s[r] * (v[r] * w.q[r]);
   }
 }
 
@@ -913,19 +940,20 @@ __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&
   for (int mb = 0; mb < 4; ++mb) {
     Layer0Weights w0;
     if (kFromLayer0) w0 = layer0_weights(s_small, mb, g);
+    f4 zv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) zv[r] = kFromLayer0 ? layer0_zv(w0, r, x0, x1) : zp[mb][0][r];
+    tanh_scaled4(zv, pv[mb], ps[mb]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      float v, sl, l;
+      const float v = pv[mb][r], sl = ps[mb][r];
+      float l;
       if (kFromLayer0) {
-        tanh_scaled(layer0_zv(w0, r, x0, x1), v, sl);
         l = sl * (v * w0.q[r]);
       } else {
-        tanh_scaled(zp[mb][0][r], v, sl);
         const float q = __builtin_fmaf(zp[mb][1][r], zp[mb][1][r], zp[mb][2][r] * zp[mb][2][r]);
         l = sl * __builtin_fmaf(v, q, zp[mb][3][r]);
       }
-      pv[mb][r] = v;
-      ps[mb][r] = sl;
       stage_write(stage_lane, mb, r, zbar[mb][0][r], zbar[mb][3][r], v, l);
     }
   }
