@@ -40,6 +40,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -2000,16 +2001,20 @@ int check_launch(const char* what) {
   return FHOAD_SUCCESS;
 }
 
-// Compute units of the current device, queried once per device.
+// Compute units of the current device, queried once per device. The cache entries are atomic:
+// calls from several host threads may fill the same entry (with the same value).
 int current_device_cus(int* cus) {
   constexpr int kMaxDevices = 64;
-  static int cached[kMaxDevices] = {};
+  static std::atomic<int> cached[kMaxDevices] = {};
   int device = 0;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return fail(FHOAD_ERROR_DEVICE, "hipGetDevice: %s", hipGetErrorString(err));
-  if (device >= 0 && device < kMaxDevices && cached[device] > 0) {
-    *cus = cached[device];
-    return FHOAD_SUCCESS;
+  if (device >= 0 && device < kMaxDevices) {
+    const int known = cached[device].load(std::memory_order_relaxed);
+    if (known > 0) {
+      *cus = known;
+      return FHOAD_SUCCESS;
+    }
   }
   int count = 0;
   err = hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device);
@@ -2017,7 +2022,7 @@ int current_device_cus(int* cus) {
     return fail(FHOAD_ERROR_DEVICE, "hipDeviceGetAttribute: %s", hipGetErrorString(err));
   }
   if (count < 1) count = 1;
-  if (device >= 0 && device < kMaxDevices) cached[device] = count;
+  if (device >= 0 && device < kMaxDevices) cached[device].store(count, std::memory_order_relaxed);
   *cus = count;
   return FHOAD_SUCCESS;
 }
