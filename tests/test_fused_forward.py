@@ -30,9 +30,10 @@ def _fused(x, p, version=2):
     return fused_forward_laplacian(x, p, version)
 
 
-# the reference's tile edges (test_fused.py:28) plus this kernel's: 16-point wave tiles
+# the reference's tile edges (test_fused.py:28) plus this kernel's: 16-point wave tiles, and
+# ragged large batches (a partial last tile, workgroups with unequal tile counts)
 @pytest.mark.parametrize(
-    "batch", [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 4097, 16384, 65536]
+    "batch", [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 4097, 16384, 65536, 65537, 262145]
 )
 def test_forward_matches_torch_forward_laplacian(batch: int) -> None:
     announce(f"forward vs torch forward Laplacian, batch={batch}")

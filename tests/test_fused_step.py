@@ -266,7 +266,8 @@ def _boundary(count: int, seed: int):
 
 @pytest.mark.parametrize(
     "batch,nb",
-    [(1000, 100), (100, 1), (100, 63), (64, 64), (100, 65), (12000, 288), (12000, 289), (20000, 1024)],
+    [(1000, 100), (100, 1), (100, 63), (64, 64), (100, 65), (12000, 288), (12000, 289), (20000, 1024),
+     (65537, 1025)],
 )
 def test_pinn_step_with_boundary_matches_the_oracle(batch: int, nb: int) -> None:
     announce(f"fused PINN+Adam step (boundary term) vs float64 oracle, batch={batch}, boundary={nb}")
