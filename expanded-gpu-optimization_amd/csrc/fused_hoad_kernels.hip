@@ -127,6 +127,21 @@ __device__ __forceinline__ void tanh_scaled4(const f4 zv, f4& v, f4& s) {
   }
 }
 
+// tanh_jet of four values (component vectors z[c][r] of one accumulator row block), the tanh
+// four at a time (tanh_scaled4): out[c][r] is the scaled output jet.
+__device__ __forceinline__ void tanh_jet4(const f4 (&z)[4], f4 (&out)[4]) {
+  f4 v, sl;
+  tanh_scaled4(z[0], v, sl);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float q = __builtin_fmaf(z[1][r], z[1][r], z[2][r] * z[2][r]);
+    out[0][r] = v[r];
+    out[1][r] = sl[r] * z[1][r];
+    out[2][r] = sl[r] * z[2][r];
+    out[3][r] = sl[r] * __builtin_fmaf(v[r], q, z[3][r]);
+  }
+}
+
 // Forward tanh jet in scaled variables: (c z_v, z_J0, z_J1, lambda z_L) ->
 // (c v, J0, J1, lambda L) with v = tanh z_v, J = s z_J, L = s z_L - 2 v s q, q = |z_J|^2.
 __device__ __forceinline__ void tanh_jet(float zv, float zj0, float zj1, float zl, float& v,
@@ -1666,15 +1681,7 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
             }
           }
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float v, j0, j1, l;
-          tanh_jet(z[layer][0][r], z[layer][1][r], z[layer][2][r], z[layer][3][r], v, j0, j1, l);
-          mine[0][r] = v;
-          mine[1][r] = j0;
-          mine[2][r] = j1;
-          mine[3][r] = l;
-        }
+        tanh_jet4(z[layer], mine);
         f4 (*xb)[4][kWave] = s_x[phase];
         phase ^= 1;
 #pragma unroll
@@ -1735,10 +1742,11 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
       for (int layer = 2; layer >= 0; --layer) {
         // zbar of this wave's rows (tanh-jet adjoint, lane-local)
         f4 zb[4];
+        f4 v4, s4;
+        tanh_scaled4(z[layer][0], v4, s4);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float v, s;
-          tanh_scaled(z[layer][0][r], v, s);
+          const float v = v4[r], s = s4[r];
           float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
           tanh_jet_adjoint_vs(v, s, z[layer][1][r], z[layer][2][r], z[layer][3][r], bv, bj0, bj1,
                               bl);
@@ -1799,10 +1807,13 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
         const Layer0Weights w0 = layer0_weights(s_small, w, g);
         const float cx0 = kC * x0, cx1 = kC * x1;
         float gx0 = 0.f, gx1 = 0.f;
+        f4 zv4, v4, s4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) zv4[r] = layer0_zv(w0, r, x0, x1);
+        tanh_scaled4(zv4, v4, s4);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float v, s;
-          tanh_scaled(layer0_zv(w0, r, x0, x1), v, s);
+          const float v = v4[r], s = s4[r];
           float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
           tanh_jet_adjoint_vs(v, s, w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
           gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
