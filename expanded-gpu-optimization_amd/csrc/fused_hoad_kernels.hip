@@ -127,6 +127,40 @@ __device__ __forceinline__ void tanh_scaled4(const f4 zv, f4& v, f4& s) {
   }
 }
 
+// tanh of four values in the quarter-scaled jet of the forward kernels. Input zv = c z_v;
+// outputs v = (c / 4) tanh(z_v) and s = (1 - tanh^2 z_v) / 4. With t = exp(-2 z_v) = exp2(zv)
+// and u = 1 / (1 + t):
+//   tanh z_v = 2 u - 1,   1 - tanh^2 z_v = 4 u (1 - u),
+// so v = fma(u, c / 2, -c / 4) and s = fma(-u, u, u): 3 VALU + 2 transcendental instructions,
+// two fewer than tanh_scaled, as no sign needs restoring. t overflows to +inf for z_v < -44
+// (u = 0: tanh = -1, s = 0) and flushes to 0 for z_v > 44 (u = 1: tanh = 1, s = 0). Near
+// tanh = +1, s carries the absolute rounding of u (about 6e-8), as 1 - a^2 does. Staged like
+// tanh_scaled4: the four exp2, then the four rcp, then the rest.
+__device__ __forceinline__ void tanh_quarter4(const f4 zv, f4& v, f4& s) {
+  f4 u;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) u[r] = __builtin_amdgcn_exp2f(zv[r]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) u[r] = __builtin_amdgcn_rcpf(u[r] + 1.0f);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    v[r] = __builtin_fmaf(u[r], 0.5f * kC, -0.25f * kC);
+    s[r] = __builtin_fmaf(-u[r], u[r], u[r]);
+  }
+}
+
+// (v, s) of four values in the jet scaling kQuarter selects (tanh_quarter4 or tanh_scaled4).
+template <bool kQuarter>
+__device__ __forceinline__ void tanh_vs4(const f4 zv, f4& v, f4& s) {
+  if constexpr (kQuarter) {
+    tanh_quarter4(zv, v, s);
+  } else {
+    tanh_scaled4(zv, v, s);
+  }
+}
+
 // tanh_jet of four values (component vectors z[c][r] of one accumulator row block), the tanh
 // four at a time (tanh_scaled4): out[c][r] is the scaled output jet.
 __device__ __forceinline__ void tanh_jet4(const f4 (&z)[4], f4 (&out)[4]) {
@@ -217,21 +251,26 @@ __device__ __forceinline__ void tanh_jet_adjoint_layer0(float v, float s, float 
   bl = s * bl;
 }
 
-// Small-parameter staging shared by both kernels (see kSmallCwx for the scaled forms).
+// Small-parameter staging shared by all kernels (see kSmallCwx for the scaled forms). In the
+// quarter-scaled jet (kQuarter) the layer-0 z_J are staged as 2 W0 columns, their squared norm
+// as 4 |W0 row|^2, and w_out as 4 w_out / c and 4 w_out / lambda (exact power-of-two factors).
+template <bool kQuarter = false>
 __device__ __forceinline__ void stage_small(const float* __restrict__ params, float* s_small,
                                             int tid, int threads) {
+  constexpr float kJ = kQuarter ? 2.0f : 1.0f;
+  constexpr float kOut = kQuarter ? 4.0f : 1.0f;
   for (int o = tid; o < kHidden; o += threads) {
     const float wx = params[kInputs * o];
     const float wy = params[kInputs * o + 1];
     s_small[kSmallCwx + o] = kC * wx;
     s_small[kSmallCwy + o] = kC * wy;
     s_small[kSmallCb0 + o] = kC * params[kLayer0Bias + o];
-    s_small[kSmallWx + o] = wx;
-    s_small[kSmallWy + o] = wy;
-    s_small[kSmallQ0 + o] = __builtin_fmaf(wx, wx, wy * wy);
+    s_small[kSmallWx + o] = kJ * wx;
+    s_small[kSmallWy + o] = kJ * wy;
+    s_small[kSmallQ0 + o] = kJ * kJ * __builtin_fmaf(wx, wx, wy * wy);
     const float wo = params[kOutputBase + o];
-    s_small[kSmallWoutV + o] = wo * (1.0f / kC);
-    s_small[kSmallWoutL + o] = wo * (1.0f / kLambda);
+    s_small[kSmallWoutV + o] = kOut * (wo * (1.0f / kC));
+    s_small[kSmallWoutL + o] = kOut * (wo * (1.0f / kLambda));
   }
   for (int k = tid; k < 3 * kHidden; k += threads) {
     const int layer = k >> 6;
@@ -289,9 +328,10 @@ __device__ __forceinline__ void stage_parameters(const float* __restrict__ param
 
 // Forward-only LDS layout of the hidden weights, in MFMA operand order: for hidden layer l,
 // k-step (ob, j) and lane (m, g), the 16 bytes at f4 index (16 l + 4 ob + j) * 64 + lane hold
-// W[16 mb + m][16 ob + 4 g + j] for mb = 0..3. One ds_read_b128 per k-step feeds the 4 MFMAs
-// of that step; the 64 lanes read 1 KB contiguously (no bank conflicts) and every k-step offset
-// is an instruction immediate.
+// 4 W[16 mb + m][16 ob + 4 g + j] for mb = 0..3 (the quarter-scaled jet's weights, see
+// forward_kernel). One ds_read_b128 per k-step feeds the 4 MFMAs of that step; the 64 lanes
+// read 1 KB contiguously (no bank conflicts) and every k-step offset is an instruction
+// immediate.
 constexpr int kOperandLayerF4 = 16 * kWave;  // f4 entries per layer (16 KB)
 
 // In this layout the bank of W[o][i] (4-byte banks, 32 of them) is (4 m + mb) mod 32 with
@@ -306,7 +346,7 @@ __device__ __forceinline__ void stage_operand_weights(const float* __restrict__ 
   constexpr int kPerThread = (kQuads + kThreads - 1) / kThreads;
   auto put = [&](int layer, int o, int i, float value) {
     const int mb = o >> 4, m = o & 15, ob = i >> 4, g = (i >> 2) & 3, j = i & 3;
-    s_wa[((layer * 16 + ob * 4 + j) * kWave + 16 * g + m) * 4 + mb] = value;
+    s_wa[((layer * 16 + ob * 4 + j) * kWave + 16 * g + m) * 4 + mb] = 4.0f * value;
   };
   if ((reinterpret_cast<uintptr_t>(params) & 15) == 0) {
     f4 v[kPerThread];
@@ -474,12 +514,14 @@ __device__ __forceinline__ void hidden_layer(const float* s_small, const float* 
   hidden_product(w_rows + layer * kPlane, h, bias, acc);
 }
 
-// tanh_jet over a layer's 16 values per lane, the tanh four at a time (tanh_scaled4).
+// tanh_jet over a layer's 16 values per lane, the tanh four at a time (quarter-scaled jet if
+// kQuarter).
+template <bool kQuarter = false>
 __device__ __forceinline__ void apply_tanh_jet(const f4 (&z)[4][4], f4 (&h)[4][4]) {
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     f4 v, sl;
-    tanh_scaled4(z[mb][0], v, sl);
+    tanh_vs4<kQuarter>(z[mb][0], v, sl);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float zj0 = z[mb][1][r], zj1 = z[mb][2][r];
@@ -515,14 +557,16 @@ __device__ __forceinline__ void apply_tanh_jet_vs(const f4 (&z)[4][4], f4 (&h)[4
 
 // Layer 0 in closed form: the input jet is (x, I, 0), so z_J = W0 columns and z_L = 0, and
 // the tanh jet's q = |z_J|^2 is a per-neuron constant.
-// One block: the jet of neurons 16 mb + 4 g + r, r = 0..3, in h[c][r].
+// One block: the jet of neurons 16 mb + 4 g + r, r = 0..3, in h[c][r]. kQuarter selects the
+// quarter-scaled jet (with s_small staged by stage_small<true>).
+template <bool kQuarter = false>
 __device__ __forceinline__ void layer0_block(const float* s_small, int mb, int g, float x0,
                                              float x1, f4 (&h)[4]) {
   const Layer0Weights w = layer0_weights(s_small, mb, g);
   f4 zv, v, s;
 #pragma unroll
   for (int r = 0; r < 4; ++r) zv[r] = layer0_zv(w, r, x0, x1);
-  tanh_scaled4(zv, v, s);
+  tanh_vs4<kQuarter>(zv, v, s);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     h[0][r] = v[r];
@@ -532,10 +576,11 @@ __device__ __forceinline__ void layer0_block(const float* s_small, int mb, int g
   }
 }
 
+template <bool kQuarter = false>
 __device__ __forceinline__ void layer0_forward(const float* s_small, int g, float x0, float x1,
                                                f4 (&h)[4][4]) {
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) layer0_block(s_small, mb, g, x0, x1, h[mb]);
+  for (int mb = 0; mb < 4; ++mb) layer0_block<kQuarter>(s_small, mb, g, x0, x1, h[mb]);
 }
 
 // An opaque copy of a value: the compiler cannot see that it equals the input, so it cannot
@@ -633,6 +678,14 @@ __device__ __forceinline__ float row_reduce_scatter16(const float (&v)[16], int 
 // /root/reference/csrc/fused_residual.cu:157-295). A grid of at most one workgroup per CU
 // stages the weights once, then every wave walks 16-point tiles: tile t goes to workgroup
 // t % grid, wave (t / grid) % kWaves, so small batches still spread over all CUs.
+//
+// Quarter-scaled jet. The forward kernels carry (c v / 4, J / 2, J / 2, lambda L / 4) and the
+// hidden weights as 4 W (exact in FP32), so each layer's scales repeat:
+//   z'_v = 4 W (c v / 4) + c b = c z_v,   z'_J = 4 W (J / 2) = 2 z_J,   z'_L = lambda z_L,
+// and with s' = s / 4 and q' = |z'_J|^2 = 4 q the tanh jet keeps its form,
+//   J' = s' z'_J = J / 2,   L' = s' (z'_L + v' q') = (s / 4) lambda (z_L - 2 v q) = lambda L / 4,
+// while tanh_quarter4 forms (v', s') in 5 instructions instead of tanh_scaled4's 7: 16 values
+// per lane per layer, about an eighth of the kernel's VALU work.
 template <int kWaves>
 __global__ void __launch_bounds__(kWaves * kWave)
 forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
@@ -654,7 +707,7 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
     next_x1 = coordinates[2 * (tile * kTile + m) + 1];
   }
   stage_operand_weights<kWaves * kWave>(params, s_wa, threadIdx.x);
-  stage_small(params, s_small, threadIdx.x, kWaves * kWave);
+  stage_small<true>(params, s_small, threadIdx.x, kWaves * kWave);
   __syncthreads();
   next_x0 = opaque(next_x0);  // delivered before the loop, for the same reason as below
   next_x1 = opaque(next_x1);
@@ -672,21 +725,21 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
     }
     f4 first = wa_lane[0];
     f4 h[4][4];
-    layer0_forward(s_small, g, x0, x1, h);
+    layer0_forward<true>(s_small, g, x0, x1, h);
     for (int layer = 0; layer < 3; ++layer) {
       f4 bias[4];
       load_bias(s_small, layer, g, bias);
       f4 acc[4][4];
       hidden_product_native(wa_lane + layer * kOperandLayerF4, h, bias, acc, first);
       if (layer < 2) first = wa_lane[(layer + 1) * kOperandLayerF4];
-      apply_tanh_jet(acc, h);
+      apply_tanh_jet<true>(acc, h);
     }
     // Take delivery of the next coordinates here, before this tile's stores: a wait at the
     // top of the next tile would also wait for those stores (they sit behind a branch, so the
     // compiler cannot count them), and a store takes far longer than a tile's head.
     next_x0 = opaque(next_x0);
     next_x1 = opaque(next_x1);
-    // u = w_out . v + b_out and lap = w_out . L, from the scaled jet.
+    // u = w_out . v + b_out and lap = w_out . L, from the quarter-scaled jet.
     float u = 0.0f, lap = 0.0f;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
@@ -729,14 +782,15 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
                      int64_t tiles) {
   __shared__ f4 s_h[2][kSplitWaves][4][kWave];  // [buffer][wave][component][lane], 32 KB
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
-  stage_small(params, s_small, threadIdx.x, kSplitWaves * kWave);
+  stage_small<true>(params, s_small, threadIdx.x, kSplitWaves * kWave);
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int m = lane & 15;
   const int g = lane >> 4;
-  // A operands of this wave's rows: wa[l][ob][j] = W_l[16 w + m][16 ob + 4 g + j], loaded once
-  // (global memory, L2-resident) instead of staging the whole matrix in LDS.
+  // A operands of this wave's rows: wa[l][ob][j] = 4 W_l[16 w + m][16 ob + 4 g + j] (the
+  // quarter-scaled jet's weights), loaded once (global memory, L2-resident) instead of staging
+  // the whole matrix in LDS.
   f4 wa[3][4];
   {
     const float* row = params + kHiddenBase + (16 * w + m) * kHidden + 4 * g;
@@ -746,7 +800,7 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
 #pragma unroll
       for (int ob = 0; ob < 4; ++ob) {
         const float* p = row + l * kHiddenStride + 16 * ob;
-        wa[l][ob] = aligned ? *reinterpret_cast<const f4*>(p) : f4{p[0], p[1], p[2], p[3]};
+        wa[l][ob] = 4.0f * (aligned ? *reinterpret_cast<const f4*>(p) : f4{p[0], p[1], p[2], p[3]});
       }
     }
   }
@@ -763,7 +817,7 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
       x1 = coordinates[2 * point + 1];
     }
     f4 h[4][4];
-    layer0_forward(s_small, g, x0, x1, h);
+    layer0_forward<true>(s_small, g, x0, x1, h);
 #pragma unroll
     for (int layer = 0; layer < 3; ++layer) {
       const f4 bias = lds4(s_small + kSmallBh + layer * kHidden + 16 * w + 4 * g);
@@ -780,14 +834,17 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
         }
       }
       f4 mine[4];
+      {
+        f4 v, sl;
+        tanh_quarter4(acc[0], v, sl);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v, j0, j1, l;
-        tanh_jet(acc[0][r], acc[1][r], acc[2][r], acc[3][r], v, j0, j1, l);
-        mine[0][r] = v;
-        mine[1][r] = j0;
-        mine[2][r] = j1;
-        mine[3][r] = l;
+        for (int r = 0; r < 4; ++r) {
+          const float q = __builtin_fmaf(acc[1][r], acc[1][r], acc[2][r] * acc[2][r]);
+          mine[0][r] = v[r];
+          mine[1][r] = sl[r] * acc[1][r];
+          mine[2][r] = sl[r] * acc[2][r];
+          mine[3][r] = sl[r] * __builtin_fmaf(v[r], q, acc[3][r]);
+        }
       }
       f4 (*buf)[4][kWave] = s_h[phase];
       phase ^= 1;
