@@ -21,15 +21,21 @@
 // is already in the operand layout of the next layer, and the tanh-jet update (which needs the
 // 4 components of one (neuron, point)) is local to a lane. Only the weights come from LDS.
 //
-// Scaled jet. Kernels carry (c v, J0, J1, lambda L) with c = -2 log2(e) and lambda = log2(e),
-// and pre-activations scaled the same way (the value bias is staged as c b). Then
-// exp(-2 |z_v|) is exp2(-|c z_v|) with no multiply, the value output c tanh(z_v) comes out of
-// one fma, and the Laplacian update is L' = s (z_L' + v' q) with v' = c tanh z_v (because
-// -2 lambda = c). w_out is staged as w_out / c and w_out / lambda for u and lap. Products of a
-// primal and its adjoint are scale-invariant, so dW and W^T zbar need no correction; bias
-// and layer-0 gradients pick up one factor c. FP32 MFMA runs on the same SIMD issue slots as
-// VALU work on gfx950 (measured: they do not co-execute), so every VALU instruction saved in
-// the jet update is MFMA time recovered.
+// Scaled jet. With c = -2 log2(e) and lambda = log2(e), kernels carry the layer outputs as
+//   (v', J0', J1', L') = (c v / 4, J0 / 2, J1 / 2, lambda L / 4)
+// and stage the hidden weights as 4 W and the value biases as c b (exact power-of-two factors
+// aside from c). The pre-activations then come out of the MFMAs as
+//   z'_v = 4 W (c v / 4) + c b = c z_v,   z'_J = 4 W (J / 2) = 2 z_J,   z'_L = lambda z_L,
+// and with s' = s / 4 and q' = |z'_J|^2 = 4 q the tanh jet keeps its form:
+//   v' = (c / 4) tanh z_v,   J' = s' z'_J,   L' = s' (z'_L + v' q') = lambda L / 4
+// (because c = -2 lambda), with the same scales at every layer. exp(-2 z_v) is exp2(z'_v) with
+// no multiply, and (v', s') take 3 VALU + 2 transcendental instructions (tanh_scaled). Layer 0
+// uses z'_J = 2 W0 columns; w_out is staged as 4 w_out / c and 4 w_out / lambda for u and lap.
+// The backward is backpropagation through this scaled network (weights 4 W): its dW sums are
+// of d/d(4 W), so the partial rows take a factor 4; bias gradients take c; layer-0 weight
+// gradients c for the x terms and 2 for the z_J terms. FP32 MFMA runs on the same SIMD issue
+// slots as VALU work on gfx950 (measured: they do not co-execute), so every VALU instruction
+// saved in the jet update is MFMA time recovered.
 //
 // LDS weight layouts. The forward kernel keeps W in MFMA operand order (one 16-byte read per
 // k-step, see stage_operand_weights); its small-batch form (forward_split_kernel) keeps only a
@@ -61,20 +67,20 @@ constexpr int kPlane = 4352;  // floats per 64 x 68 LDS plane
 
 // Scale factors of the carried jet (see the header comment).
 constexpr float kC = -2.8853900817779268f;       // c = -2 log2(e)
-constexpr float kAbsC = 2.8853900817779268f;     // |c|
 constexpr float kLambda = 1.4426950408889634f;   // lambda = log2(e)
-constexpr float kKappa = -0.24022650695910071f;  // -2 / c^2
+constexpr float kKappa = -0.96090602783640284f;  // -8 / c^2 (tanh_jet_adjoint_vs)
+constexpr float kHalfC = 0.5f * kC;              // c / 2 (layer-0 weight gradients)
 
 // Small parameter blocks in LDS (float offsets inside s_small), each [64] over neurons.
 constexpr int kSmallCwx = 0;                       // c W0[:, 0]
 constexpr int kSmallCwy = kSmallCwx + kHidden;     // c W0[:, 1]
 constexpr int kSmallCb0 = kSmallCwy + kHidden;     // c b0
-constexpr int kSmallWx = kSmallCb0 + kHidden;      // W0[:, 0]
-constexpr int kSmallWy = kSmallWx + kHidden;       // W0[:, 1]
-constexpr int kSmallQ0 = kSmallWy + kHidden;       // W0[:, 0]^2 + W0[:, 1]^2
+constexpr int kSmallWx = kSmallCb0 + kHidden;      // 2 W0[:, 0] (layer 0's z'_J0)
+constexpr int kSmallWy = kSmallWx + kHidden;       // 2 W0[:, 1]
+constexpr int kSmallQ0 = kSmallWy + kHidden;       // 4 (W0[:, 0]^2 + W0[:, 1]^2) = |z'_J|^2
 constexpr int kSmallBh = kSmallQ0 + kHidden;       // c b1..b3, [3][64]
-constexpr int kSmallWoutV = kSmallBh + 3 * kHidden;  // w_out / c
-constexpr int kSmallWoutL = kSmallWoutV + kHidden;   // w_out / lambda
+constexpr int kSmallWoutV = kSmallBh + 3 * kHidden;  // 4 w_out / c
+constexpr int kSmallWoutL = kSmallWoutV + kHidden;   // 4 w_out / lambda
 constexpr int kSmallBout = kSmallWoutL + kHidden;    // b_out
 constexpr int kSmallFloats = kSmallBout + 4;
 
@@ -91,52 +97,25 @@ __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
 
 __device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
-// tanh in the scaled jet. Input zv = c z_v; outputs v = c tanh(z_v) and s = 1 - tanh^2 z_v.
-// With t = exp(-2|z_v|) = exp2(-|zv|) and u = 2 / (1 + t) = 1 + |tanh z_v|:
-//   1 - |tanh z_v| = t u,   s = (1 + |tanh|)(1 - |tanh|) = u (t u),
-//   |v| = |c| (1 - t u),    sign(v) = sign(c z_v) = sign(zv).
-// Derived from tanh z = (1 - e^{-2z}) / (1 + e^{-2z}) on v_exp_f32 / v_rcp_f32; s has no
-// 1 - a^2 cancellation, so it keeps its relative accuracy where tanh saturates, and t flushes to
-// 0 for |z_v| > ~44 (tanh = +-1, s = 0). 5 VALU + 2 transcendental instructions.
+// tanh in the scaled jet. Input zv = c z_v; outputs v = (c / 4) tanh(z_v) and
+// s = (1 - tanh^2 z_v) / 4. With t = exp(-2 z_v) = exp2(zv) and u = 1 / (1 + t):
+//   tanh z_v = 2 u - 1,   1 - tanh^2 z_v = 4 u (1 - u),
+// so v = fma(u, c / 2, -c / 4) and s = fma(-u, u, u): 3 VALU + 2 transcendental instructions
+// (v_exp_f32, v_rcp_f32). t overflows to +inf for z_v < -44 (u = 0: tanh = -1, s = 0) and
+// flushes to 0 for z_v > 44 (u = 1: tanh = 1, s = 0). Near tanh = +1, s carries the absolute
+// rounding of u (about 6e-8), as 1 - a^2 does.
 __device__ __forceinline__ void tanh_scaled(float zv, float& v, float& s) {
-  const float t = __builtin_amdgcn_exp2f(-__builtin_fabsf(zv));
-  const float u = __builtin_amdgcn_rcpf(__builtin_fmaf(t, 0.5f, 0.5f));
-  const float w = t * u;
-  s = u * w;
-  v = __builtin_copysignf(__builtin_fmaf(w, -kAbsC, kAbsC), zv);
+  const float u = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(zv) + 1.0f);
+  v = __builtin_fmaf(u, 0.5f * kC, -0.25f * kC);
+  s = __builtin_fmaf(-u, u, u);
 }
 
 // tanh_scaled of four values, in stages across the four: the four exp2, then the four rcp, then
 // the rest, with fences so the scheduler keeps the stages. Each value's chain is serial
-// (exp2 -> fma -> rcp -> mul), and left alone the compiler ran the chains one after another
-// with two temporaries; a wave alone on its SIMD (the backward, the forward's last tiles) then
-// waited out every transcendental's latency. Same operations per value as tanh_scaled.
+// (exp2 -> add -> rcp -> fma), and left alone the compiler ran the chains one after another;
+// a wave alone on its SIMD (the backward, the forward's last tiles) then waited out every
+// transcendental's latency. Same operations per value as tanh_scaled.
 __device__ __forceinline__ void tanh_scaled4(const f4 zv, f4& v, f4& s) {
-  f4 t, u;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) t[r] = __builtin_amdgcn_exp2f(-__builtin_fabsf(zv[r]));
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) u[r] = __builtin_amdgcn_rcpf(__builtin_fmaf(t[r], 0.5f, 0.5f));
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float w = t[r] * u[r];
-    s[r] = u[r] * w;
-    v[r] = __builtin_copysignf(__builtin_fmaf(w, -kAbsC, kAbsC), zv[r]);
-  }
-}
-
-// tanh of four values in the quarter-scaled jet of the forward kernels. Input zv = c z_v;
-// outputs v = (c / 4) tanh(z_v) and s = (1 - tanh^2 z_v) / 4. With t = exp(-2 z_v) = exp2(zv)
-// and u = 1 / (1 + t):
-//   tanh z_v = 2 u - 1,   1 - tanh^2 z_v = 4 u (1 - u),
-// so v = fma(u, c / 2, -c / 4) and s = fma(-u, u, u): 3 VALU + 2 transcendental instructions,
-// two fewer than tanh_scaled, as no sign needs restoring. t overflows to +inf for z_v < -44
-// (u = 0: tanh = -1, s = 0) and flushes to 0 for z_v > 44 (u = 1: tanh = 1, s = 0). Near
-// tanh = +1, s carries the absolute rounding of u (about 6e-8), as 1 - a^2 does. Staged like
-// tanh_scaled4: the four exp2, then the four rcp, then the rest.
-__device__ __forceinline__ void tanh_quarter4(const f4 zv, f4& v, f4& s) {
   f4 u;
 #pragma unroll
   for (int r = 0; r < 4; ++r) u[r] = __builtin_amdgcn_exp2f(zv[r]);
@@ -148,16 +127,6 @@ __device__ __forceinline__ void tanh_quarter4(const f4 zv, f4& v, f4& s) {
   for (int r = 0; r < 4; ++r) {
     v[r] = __builtin_fmaf(u[r], 0.5f * kC, -0.25f * kC);
     s[r] = __builtin_fmaf(-u[r], u[r], u[r]);
-  }
-}
-
-// (v, s) of four values in the jet scaling kQuarter selects (tanh_quarter4 or tanh_scaled4).
-template <bool kQuarter>
-__device__ __forceinline__ void tanh_vs4(const f4 zv, f4& v, f4& s) {
-  if constexpr (kQuarter) {
-    tanh_quarter4(zv, v, s);
-  } else {
-    tanh_scaled4(zv, v, s);
   }
 }
 
@@ -176,26 +145,17 @@ __device__ __forceinline__ void tanh_jet4(const f4 (&z)[4], f4 (&out)[4]) {
   }
 }
 
-// Forward tanh jet in scaled variables: (c z_v, z_J0, z_J1, lambda z_L) ->
-// (c v, J0, J1, lambda L) with v = tanh z_v, J = s z_J, L = s z_L - 2 v s q, q = |z_J|^2.
-__device__ __forceinline__ void tanh_jet(float zv, float zj0, float zj1, float zl, float& v,
-                                         float& j0, float& j1, float& l) {
-  float s;
-  tanh_scaled(zv, v, s);
-  const float q = __builtin_fmaf(zj0, zj0, zj1 * zj1);
-  j0 = s * zj0;
-  j1 = s * zj1;
-  l = s * __builtin_fmaf(v, q, zl);
-}
-
-// Adjoint of tanh_jet in the same scaled variables (the adjoint of a scaled quantity is the
-// unscaled adjoint divided by the scale). With v' = c tanh z_v, P = z_L' + v' q and
-// kappa = -2 / c^2 (so d s / d(c z_v) = kappa v' s):
-//   zbar_v' = s [vbar' + kappa v' (Jbar . z_J) + Lbar' (kappa v' P + s q)]
-//   zbar_Jd = s (Jbar_d + 2 Lbar' v' z_Jd)
-//   zbar_L' = s Lbar'
+// Adjoint of the tanh jet (tanh_jet4, per value) in the scaled variables (the adjoint of a
+// scaled quantity is the unscaled adjoint divided by the scale). With v' = (c / 4) tanh z_v,
+// s' = s / 4, z'_J = 2 z_J, q' = |z'_J|^2, P = z'_L + v' q' and kappa = -8 / c^2 (so
+// d s' / d(c z_v) = kappa v' s'):
+//   zbar_v' = s' [vbar' + kappa v' (Jbar' . z'_J) + Lbar' (kappa v' P + s' q')]
+//   zbar_Jd' = s' (Jbar_d' + 2 Lbar' v' z'_Jd)
+//   zbar_L' = s' Lbar'
+// the unscaled formulas with every quantity replaced by its scaled form (the factors cancel).
 // This is the reference's tanh_backward (/root/reference/csrc/fused_backward.cu:29-33, 75-89)
-// rewritten for the scaled jet. The adjoint (vbar', J0bar, J1bar, Lbar') is replaced in place.
+// rewritten for the scaled jet. The adjoint (vbar', J0bar', J1bar', Lbar') is replaced in
+// place.
 __device__ __forceinline__ void tanh_jet_adjoint_vs(float v, float s, float zj0, float zj1,
                                                     float zl, float& bv, float& bj0, float& bj1,
                                                     float& bl) {
@@ -251,26 +211,22 @@ __device__ __forceinline__ void tanh_jet_adjoint_layer0(float v, float s, float 
   bl = s * bl;
 }
 
-// Small-parameter staging shared by all kernels (see kSmallCwx for the scaled forms). In the
-// quarter-scaled jet (kQuarter) the layer-0 z_J are staged as 2 W0 columns, their squared norm
-// as 4 |W0 row|^2, and w_out as 4 w_out / c and 4 w_out / lambda (exact power-of-two factors).
-template <bool kQuarter = false>
+// Small-parameter staging shared by all kernels, in the scaled forms listed at kSmallCwx (the
+// factors 2 and 4 are exact).
 __device__ __forceinline__ void stage_small(const float* __restrict__ params, float* s_small,
                                             int tid, int threads) {
-  constexpr float kJ = kQuarter ? 2.0f : 1.0f;
-  constexpr float kOut = kQuarter ? 4.0f : 1.0f;
   for (int o = tid; o < kHidden; o += threads) {
     const float wx = params[kInputs * o];
     const float wy = params[kInputs * o + 1];
     s_small[kSmallCwx + o] = kC * wx;
     s_small[kSmallCwy + o] = kC * wy;
     s_small[kSmallCb0 + o] = kC * params[kLayer0Bias + o];
-    s_small[kSmallWx + o] = kJ * wx;
-    s_small[kSmallWy + o] = kJ * wy;
-    s_small[kSmallQ0 + o] = kJ * kJ * __builtin_fmaf(wx, wx, wy * wy);
+    s_small[kSmallWx + o] = 2.0f * wx;
+    s_small[kSmallWy + o] = 2.0f * wy;
+    s_small[kSmallQ0 + o] = 4.0f * __builtin_fmaf(wx, wx, wy * wy);
     const float wo = params[kOutputBase + o];
-    s_small[kSmallWoutV + o] = kOut * (wo * (1.0f / kC));
-    s_small[kSmallWoutL + o] = kOut * (wo * (1.0f / kLambda));
+    s_small[kSmallWoutV + o] = 4.0f * (wo * (1.0f / kC));
+    s_small[kSmallWoutL + o] = 4.0f * (wo * (1.0f / kLambda));
   }
   for (int k = tid; k < 3 * kHidden; k += threads) {
     const int layer = k >> 6;
@@ -315,21 +271,21 @@ __device__ __forceinline__ void stage_hidden(const float* __restrict__ params, i
   }
 }
 
-// Copy the packed parameters into LDS for the backward: the three hidden W into pitch-68
-// planes, the small blocks in the scaled forms listed at kSmallCwx.
+// Copy the packed parameters into LDS for the backward: the three hidden W, as 4 W (the scaled
+// jet's weights), into pitch-68 planes, the small blocks in the scaled forms listed at
+// kSmallCwx.
 template <int kThreads>
 __device__ __forceinline__ void stage_parameters(const float* __restrict__ params, float* s_w,
                                                  float* s_small, int tid) {
   stage_hidden<kThreads>(params, tid, [&](int layer, int o, int i, float value) {
-    s_w[layer * kPlane + kWRow * o + i] = value;
+    s_w[layer * kPlane + kWRow * o + i] = 4.0f * value;
   });
   stage_small(params, s_small, tid, kThreads);
 }
 
 // Forward-only LDS layout of the hidden weights, in MFMA operand order: for hidden layer l,
 // k-step (ob, j) and lane (m, g), the 16 bytes at f4 index (16 l + 4 ob + j) * 64 + lane hold
-// 4 W[16 mb + m][16 ob + 4 g + j] for mb = 0..3 (the quarter-scaled jet's weights, see
-// forward_kernel). One ds_read_b128 per k-step feeds the 4 MFMAs of that step; the 64 lanes
+// 4 W[16 mb + m][16 ob + 4 g + j] for mb = 0..3 (the scaled jet's weights). One ds_read_b128 per k-step feeds the 4 MFMAs of that step; the 64 lanes
 // read 1 KB contiguously (no bank conflicts) and every k-step offset is an instruction
 // immediate.
 constexpr int kOperandLayerF4 = 16 * kWave;  // f4 entries per layer (16 KB)
@@ -514,14 +470,12 @@ __device__ __forceinline__ void hidden_layer(const float* s_small, const float* 
   hidden_product(w_rows + layer * kPlane, h, bias, acc);
 }
 
-// tanh_jet over a layer's 16 values per lane, the tanh four at a time (quarter-scaled jet if
-// kQuarter).
-template <bool kQuarter = false>
+// tanh_jet over a layer's 16 values per lane, the tanh four at a time (tanh_scaled4).
 __device__ __forceinline__ void apply_tanh_jet(const f4 (&z)[4][4], f4 (&h)[4][4]) {
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     f4 v, sl;
-    tanh_vs4<kQuarter>(z[mb][0], v, sl);
+    tanh_scaled4(z[mb][0], v, sl);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float zj0 = z[mb][1][r], zj1 = z[mb][2][r];
@@ -557,16 +511,14 @@ __device__ __forceinline__ void apply_tanh_jet_vs(const f4 (&z)[4][4], f4 (&h)[4
 
 // Layer 0 in closed form: the input jet is (x, I, 0), so z_J = W0 columns and z_L = 0, and
 // the tanh jet's q = |z_J|^2 is a per-neuron constant.
-// One block: the jet of neurons 16 mb + 4 g + r, r = 0..3, in h[c][r]. kQuarter selects the
-// quarter-scaled jet (with s_small staged by stage_small<true>).
-template <bool kQuarter = false>
+// One block: the jet of neurons 16 mb + 4 g + r, r = 0..3, in h[c][r].
 __device__ __forceinline__ void layer0_block(const float* s_small, int mb, int g, float x0,
                                              float x1, f4 (&h)[4]) {
   const Layer0Weights w = layer0_weights(s_small, mb, g);
   f4 zv, v, s;
 #pragma unroll
   for (int r = 0; r < 4; ++r) zv[r] = layer0_zv(w, r, x0, x1);
-  tanh_vs4<kQuarter>(zv, v, s);
+  tanh_scaled4(zv, v, s);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     h[0][r] = v[r];
@@ -576,11 +528,10 @@ __device__ __forceinline__ void layer0_block(const float* s_small, int mb, int g
   }
 }
 
-template <bool kQuarter = false>
 __device__ __forceinline__ void layer0_forward(const float* s_small, int g, float x0, float x1,
                                                f4 (&h)[4][4]) {
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) layer0_block<kQuarter>(s_small, mb, g, x0, x1, h[mb]);
+  for (int mb = 0; mb < 4; ++mb) layer0_block(s_small, mb, g, x0, x1, h[mb]);
 }
 
 // An opaque copy of a value: the compiler cannot see that it equals the input, so it cannot
@@ -678,14 +629,6 @@ __device__ __forceinline__ float row_reduce_scatter16(const float (&v)[16], int 
 // /root/reference/csrc/fused_residual.cu:157-295). A grid of at most one workgroup per CU
 // stages the weights once, then every wave walks 16-point tiles: tile t goes to workgroup
 // t % grid, wave (t / grid) % kWaves, so small batches still spread over all CUs.
-//
-// Quarter-scaled jet. The forward kernels carry (c v / 4, J / 2, J / 2, lambda L / 4) and the
-// hidden weights as 4 W (exact in FP32), so each layer's scales repeat:
-//   z'_v = 4 W (c v / 4) + c b = c z_v,   z'_J = 4 W (J / 2) = 2 z_J,   z'_L = lambda z_L,
-// and with s' = s / 4 and q' = |z'_J|^2 = 4 q the tanh jet keeps its form,
-//   J' = s' z'_J = J / 2,   L' = s' (z'_L + v' q') = (s / 4) lambda (z_L - 2 v q) = lambda L / 4,
-// while tanh_quarter4 forms (v', s') in 5 instructions instead of tanh_scaled4's 7: 16 values
-// per lane per layer, about an eighth of the kernel's VALU work.
 template <int kWaves>
 __global__ void __launch_bounds__(kWaves * kWave)
 forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
@@ -707,7 +650,7 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
     next_x1 = coordinates[2 * (tile * kTile + m) + 1];
   }
   stage_operand_weights<kWaves * kWave>(params, s_wa, threadIdx.x);
-  stage_small<true>(params, s_small, threadIdx.x, kWaves * kWave);
+  stage_small(params, s_small, threadIdx.x, kWaves * kWave);
   __syncthreads();
   next_x0 = opaque(next_x0);  // delivered before the loop, for the same reason as below
   next_x1 = opaque(next_x1);
@@ -725,21 +668,21 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
     }
     f4 first = wa_lane[0];
     f4 h[4][4];
-    layer0_forward<true>(s_small, g, x0, x1, h);
+    layer0_forward(s_small, g, x0, x1, h);
     for (int layer = 0; layer < 3; ++layer) {
       f4 bias[4];
       load_bias(s_small, layer, g, bias);
       f4 acc[4][4];
       hidden_product_native(wa_lane + layer * kOperandLayerF4, h, bias, acc, first);
       if (layer < 2) first = wa_lane[(layer + 1) * kOperandLayerF4];
-      apply_tanh_jet<true>(acc, h);
+      apply_tanh_jet(acc, h);
     }
     // Take delivery of the next coordinates here, before this tile's stores: a wait at the
     // top of the next tile would also wait for those stores (they sit behind a branch, so the
     // compiler cannot count them), and a store takes far longer than a tile's head.
     next_x0 = opaque(next_x0);
     next_x1 = opaque(next_x1);
-    // u = w_out . v + b_out and lap = w_out . L, from the quarter-scaled jet.
+    // u = w_out . v + b_out and lap = w_out . L, from the scaled jet.
     float u = 0.0f, lap = 0.0f;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
@@ -782,14 +725,14 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
                      int64_t tiles) {
   __shared__ f4 s_h[2][kSplitWaves][4][kWave];  // [buffer][wave][component][lane], 32 KB
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
-  stage_small<true>(params, s_small, threadIdx.x, kSplitWaves * kWave);
+  stage_small(params, s_small, threadIdx.x, kSplitWaves * kWave);
 
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int m = lane & 15;
   const int g = lane >> 4;
   // A operands of this wave's rows: wa[l][ob][j] = 4 W_l[16 w + m][16 ob + 4 g + j] (the
-  // quarter-scaled jet's weights), loaded once (global memory, L2-resident) instead of staging
+  // scaled jet's weights), loaded once (global memory, L2-resident) instead of staging
   // the whole matrix in LDS.
   f4 wa[3][4];
   {
@@ -817,7 +760,7 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
       x1 = coordinates[2 * point + 1];
     }
     f4 h[4][4];
-    layer0_forward<true>(s_small, g, x0, x1, h);
+    layer0_forward(s_small, g, x0, x1, h);
 #pragma unroll
     for (int layer = 0; layer < 3; ++layer) {
       const f4 bias = lds4(s_small + kSmallBh + layer * kHidden + 16 * w + 4 * g);
@@ -836,7 +779,7 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
       f4 mine[4];
       {
         f4 v, sl;
-        tanh_quarter4(acc[0], v, sl);
+        tanh_scaled4(acc[0], v, sl);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float q = __builtin_fmaf(acc[1][r], acc[1][r], acc[2][r] * acc[2][r]);
@@ -1187,7 +1130,7 @@ struct WaveSums {
 };
 
 // A boundary tile of the fused step. Boundary points enter the loss through u alone
-// (grad_lap = 0), so the output seed is (vbar, Jbar, Lbar) = (gu w_out / c, 0, 0), and the
+// (grad_lap = 0), so the output seed is (vbar', Jbar', Lbar') = (4 gu w_out / c, 0, 0), and the
 // tanh-jet adjoint maps (vbar, 0, 0, 0) to (s vbar, 0, 0, 0): every adjoint component but the
 // value one is exactly zero at every layer. The weight-gradient terms reduce to zbar_v h_v^T,
 // and the forward's J and L components feed nothing. This tile therefore runs the value
@@ -1259,7 +1202,7 @@ __device__ __forceinline__ void boundary_value_tile(const float* s_w, const floa
   const float u = active ? out + s_small[kSmallBout] : 0.0f;
   const float gu = boundary_scale * (2.0f * u);
   acc.bloss += sum_row16(u * u);
-  const float gu_c = gu * (1.0f / kC);
+  const float gu_c = gu * (4.0f / kC);
   f4 zb[4], hb[4];
   {
     float wout_terms[16];
@@ -1291,10 +1234,11 @@ __device__ __forceinline__ void boundary_value_tile(const float* s_w, const floa
                            s_stage + opaque(rows_off), s_small, w, g, x0, x1, tv, ts);
   hidden_product_t_value(s_w + opaque(cols_off), zb, hb);
 
-  // Layer 0: bv = s hbar_v; dW0[o][d] = sum_p bv (c x_d), db0 = c sum_p bv.
+  // Layer 0: bv = s' hbar_v'; dW0[o][d] = 2 sum_p bv (c x_d / 2) (the row takes the 2),
+  // db0 = c sum_p bv.
   {
     float tx[16], ty[16], tb[16];
-    const float cx0 = kC * x0, cx1 = kC * x1;
+    const float cx0 = kHalfC * x0, cx1 = kHalfC * x1;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -1472,15 +1416,16 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       }
 
       // ---- 2. output layer: w_out / b_out gradients and the adjoint seed ----
-      // In the scaled jet u = (w_out / c) . v' and lap = (w_out / lambda) . L', so
-      // dw_out = sum_p (gu / c) v' + (gl / lambda) L' and the seeds are vbar' = gu w_out / c,
-      // Lbar' = gl w_out / lambda, Jbar = 0. The point sums stay in registers (row_reduce_scatter16).
+      // In the scaled jet u = (4 w_out / c) . v' + b_out and lap = (4 w_out / lambda) . L', so
+      // dw_out = sum_p (4 gu / c) v' + (4 gl / lambda) L' and the seeds are
+      // vbar' = 4 gu w_out / c, Lbar' = 4 gl w_out / lambda, Jbar' = 0. The point sums stay in
+      // registers (row_reduce_scatter16).
       // With kLoss, gu = 0 on interior points: the value seed and the u terms are dropped
       // (their products with zero), which leaves the other results as they were.
       f4 hb[4][4];
       {
-        const float gu_c = gu * (1.0f / kC);
-        const float gl_l = gl * (1.0f / kLambda);
+        const float gu_c = gu * (4.0f / kC);
+        const float gl_l = gl * (4.0f / kLambda);
         float wout_terms[16];
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
@@ -1531,11 +1476,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       hidden_product_t(s_w + opaque(cols_off), z1, hb);
 
       // ---- 6. layer 0 in closed form ----
-      // bv is the adjoint of c z_v, so zbar_v = c bv: grad_x = (c W0)^T bv,
-      // dW0[o][d] = sum_p bv (c x_d) + zbar_Jd, db0 = c sum_p bv.
+      // bv is the adjoint of z'_v = c z_v and bj_d that of z'_Jd = 2 W0[:, d], so
+      // grad_x = (c W0)^T bv, dW0[o][d] = sum_p bv (c x_d) + 2 bj_d = 2 sum_p (bv (c x_d / 2) + bj_d)
+      // (the row takes the 2), db0 = c sum_p bv.
       {
         float gx0 = 0.f, gx1 = 0.f, tx[16], ty[16], tb[16];
-        const float cx0 = kC * x0, cx1 = kC * x1;
+        const float cx0 = kHalfC * x0, cx1 = kHalfC * x1;
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) {
           const Layer0Weights w0 = layer0_weights(s_small, mb, g);
@@ -1546,8 +1492,8 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
                                     bj1, bl);
             gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
             gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
-            tx[4 * mb + r] = __builtin_fmaf(bv, cx0, bj0);  // dW0[o][0]
-            ty[4 * mb + r] = __builtin_fmaf(bv, cx1, bj1);  // dW0[o][1]
+            tx[4 * mb + r] = __builtin_fmaf(bv, cx0, bj0);  // dW0[o][0] / 2
+            ty[4 * mb + r] = __builtin_fmaf(bv, cx1, bj1);  // dW0[o][1] / 2
             tb[4 * mb + r] = bv;                            // db0[o] / c
           }
         }
@@ -1588,9 +1534,10 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = acc.dw[l][nb][r];
+        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = 4.0f * acc.dw[l][nb][r];
       }
-      if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * acc.bh[l];  // bias sums are of c^-1 zbar_v
+      // dW: the sums are of d/d(4 W); bias sums are of zbar_v' = c^-1 zbar_v.
+      if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * acc.bh[l];
     }
     // Per-wave sums (lane = owned neuron) combined over the 4 waves in a fixed order.
     __syncthreads();  // every wave is done with the staging buffer
@@ -1611,7 +1558,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       const float* c4 = comb + q * kBwdWaves * kHidden + n;
       const float total = ((c4[0] + c4[kHidden]) + c4[2 * kHidden]) + c4[3 * kHidden];
       const int dst = q == 0 ? kInputs * n : q == 1 ? kInputs * n + 1 : q == 2 ? kLayer0Bias + n : kOutputBase + n;
-      row[dst] = q == 2 ? kC * total : total;
+      row[dst] = (q == 2 ? kC : q == 3 ? 1.0f : 2.0f) * total;  // dW0 / 2, db0 / c, dw_out
       if (threadIdx.x < (kLoss ? 3 : 1)) {
         const float* red = s_red[threadIdx.x];
         const int col = threadIdx.x == 0 ? kOutputBase + kHidden : kLossColumn + threadIdx.x - 1;
@@ -1778,8 +1725,8 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
       // ---- output layer: this wave's rows of the seed and of dw_out ----
       f4 hb[4];
       {
-        const float gu_c = gu * (1.0f / kC);
-        const float gl_l = gl * (1.0f / kLambda);
+        const float gu_c = gu * (4.0f / kC);
+        const float gl_l = gl * (4.0f / kLambda);
         const f4 wv = lds4(s_small + kSmallWoutV + 16 * w + 4 * g);
         const f4 wl = lds4(s_small + kSmallWoutL + 16 * w + 4 * g);
 #pragma unroll
@@ -1862,7 +1809,7 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
       // ---- layer 0 for this wave's rows: dW0, db0 and this wave's part of grad_x ----
       {
         const Layer0Weights w0 = layer0_weights(s_small, w, g);
-        const float cx0 = kC * x0, cx1 = kC * x1;
+        const float cx0 = kHalfC * x0, cx1 = kHalfC * x1;
         float gx0 = 0.f, gx1 = 0.f;
         f4 zv4, v4, s4;
 #pragma unroll
@@ -1905,14 +1852,14 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = dw[l][nb][r];
+        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = 4.0f * dw[l][nb][r];
       }
       if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * bias[l];
     }
     if (m < 4) {
       const int n = 16 * w + 4 * g + m;
-      row[kInputs * n] = g_w0x;
-      row[kInputs * n + 1] = g_w0y;
+      row[kInputs * n] = 2.0f * g_w0x;
+      row[kInputs * n + 1] = 2.0f * g_w0y;
       row[kLayer0Bias + n] = kC * g_b0;
       row[kOutputBase + n] = g_wout;
     }
