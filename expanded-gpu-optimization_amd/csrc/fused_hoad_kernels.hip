@@ -155,7 +155,10 @@ __device__ __forceinline__ void tanh_jet4(const f4 (&z)[4], f4 (&out)[4]) {
 // the unscaled formulas with every quantity replaced by its scaled form (the factors cancel).
 // This is the reference's tanh_backward (/root/reference/csrc/fused_backward.cu:29-33, 75-89)
 // rewritten for the scaled jet. The adjoint (vbar', J0bar', J1bar', Lbar') is replaced in
-// place.
+// place. Evaluated as
+//   zbar_L' = s' Lbar',   zbar_v' = s' [vbar' + kappa v' (Jbar' . z'_J + Lbar' P) + zbar_L' q'],
+//   zbar_Jd' = s' Jbar_d' + 2 zbar_L' v' z'_Jd
+// (17 instructions per value).
 __device__ __forceinline__ void tanh_jet_adjoint_vs(float v, float s, float zj0, float zj1,
                                                     float zl, float& bv, float& bj0, float& bj1,
                                                     float& bl) {
@@ -163,14 +166,14 @@ __device__ __forceinline__ void tanh_jet_adjoint_vs(float v, float s, float zj0,
   const float dot = __builtin_fmaf(bj0, zj0, bj1 * zj1);
   const float p = __builtin_fmaf(v, q, zl);
   const float kv = kKappa * v;
-  const float t1 = __builtin_fmaf(kv, dot, bv);
-  const float t2 = __builtin_fmaf(kv, p, s * q);
-  const float nv = s * __builtin_fmaf(bl, t2, t1);
-  const float lbv = 2.0f * bl * v;
-  bj0 = s * __builtin_fmaf(lbv, zj0, bj0);
-  bj1 = s * __builtin_fmaf(lbv, zj1, bj1);
+  const float bls = bl * s;
+  const float t = __builtin_fmaf(kv, __builtin_fmaf(bl, p, dot), bv);
+  const float nv = s * __builtin_fmaf(bls, q, t);
+  const float m2 = 2.0f * (bls * v);
+  bj0 = __builtin_fmaf(m2, zj0, s * bj0);
+  bj1 = __builtin_fmaf(m2, zj1, s * bj1);
   bv = nv;
-  bl = s * bl;
+  bl = bls;
 }
 
 // tanh_jet_adjoint_vs for the output layer's seed, whose Jbar is zero (the output feeds only
@@ -184,13 +187,14 @@ __device__ __forceinline__ void tanh_jet_adjoint_seed(float v, float s, float zj
   const float q = __builtin_fmaf(zj0, zj0, zj1 * zj1);
   const float p = __builtin_fmaf(v, q, zl);
   const float kv = kKappa * v;
-  const float t2 = __builtin_fmaf(kv, p, s * q);
-  const float nv = kZeroV ? s * (bl * t2) : s * __builtin_fmaf(bl, t2, bv);
-  const float lbv = 2.0f * bl * v;
-  bj0 = s * (lbv * zj0);
-  bj1 = s * (lbv * zj1);
+  const float bls = bl * s;
+  const float t = kZeroV ? kv * (bl * p) : __builtin_fmaf(kv, bl * p, bv);
+  const float nv = s * __builtin_fmaf(bls, q, t);
+  const float m2 = 2.0f * (bls * v);
+  bj0 = m2 * zj0;
+  bj1 = m2 * zj1;
   bv = nv;
-  bl = s * bl;
+  bl = bls;
 }
 
 // tanh_jet_adjoint_vs for layer 0, whose z_J are the W0 columns and z_L = 0: q = |z_J|^2 is
@@ -201,14 +205,14 @@ __device__ __forceinline__ void tanh_jet_adjoint_layer0(float v, float s, float 
   const float dot = __builtin_fmaf(bj0, zj0, bj1 * zj1);
   const float p = v * q;
   const float kv = kKappa * v;
-  const float t1 = __builtin_fmaf(kv, dot, bv);
-  const float t2 = __builtin_fmaf(kv, p, s * q);
-  const float nv = s * __builtin_fmaf(bl, t2, t1);
-  const float lbv = 2.0f * bl * v;
-  bj0 = s * __builtin_fmaf(lbv, zj0, bj0);
-  bj1 = s * __builtin_fmaf(lbv, zj1, bj1);
+  const float bls = bl * s;
+  const float t = __builtin_fmaf(kv, __builtin_fmaf(bl, p, dot), bv);
+  const float nv = s * __builtin_fmaf(bls, q, t);
+  const float m2 = 2.0f * (bls * v);
+  bj0 = __builtin_fmaf(m2, zj0, s * bj0);
+  bj1 = __builtin_fmaf(m2, zj1, s * bj1);
   bv = nv;
-  bl = s * bl;
+  bl = bls;
 }
 
 // Small-parameter staging shared by all kernels, in the scaled forms listed at kSmallCwx (the
