@@ -289,48 +289,36 @@ __device__ __forceinline__ void stage_parameters(const float* __restrict__ param
 
 // Forward-only LDS layout of the hidden weights, in MFMA operand order: for hidden layer l,
 // k-step (ob, j) and lane (m, g), the 16 bytes at f4 index (16 l + 4 ob + j) * 64 + lane hold
-// 4 W[16 mb + m][16 ob + 4 g + j] for mb = 0..3 (the scaled jet's weights). One ds_read_b128 per k-step feeds the 4 MFMAs of that step; the 64 lanes
-// read 1 KB contiguously (no bank conflicts) and every k-step offset is an instruction
-// immediate.
+// 4 W[16 mb + m][16 ob + 4 g + j] for mb = 0..3 (the scaled jet's weights). One ds_read_b128
+// per k-step feeds the 4 MFMAs of that step; the 64 lanes read 1 KB contiguously (no bank
+// conflicts) and every k-step offset is an instruction immediate.
 constexpr int kOperandLayerF4 = 16 * kWave;  // f4 entries per layer (16 KB)
 
-// In this layout the bank of W[o][i] (4-byte banks, 32 of them) is (4 m + mb) mod 32 with
-// o = 16 mb + m, whatever the column. The 64 lanes of a staging wave therefore take 64 different
-// rows at the same column quad (lane-per-row order), which spreads their LDS writes over all
-// banks; row-contiguous order (16 lanes per row) would put 16 lanes on one bank. Measured: the
-// staging of a 12-wave workgroup drops from 7.5K to about 2.6K cycles.
+// Staging: work item (l, ob, lane) loads the 4 x 4 block of W_l with rows m, 16 + m, 32 + m,
+// 48 + m and columns 16 ob + 4 g .. + 3 (four 16-byte global loads, all issued before the
+// first LDS write) and stores its 4 columns as the 4 k-steps (ob, j) of that lane: 16-byte LDS
+// writes, each wave's 64 of them to 1 KB contiguous, so conflict-free. 768 work items: one per
+// thread of a 12-wave workgroup.
 template <int kThreads>
 __device__ __forceinline__ void stage_operand_weights(const float* __restrict__ params, float* s_wa,
                                                       int tid) {
-  constexpr int kQuads = 3 * kHidden * kHidden / 4;  // (layer, row, column quad)
-  constexpr int kPerThread = (kQuads + kThreads - 1) / kThreads;
-  auto put = [&](int layer, int o, int i, float value) {
-    const int mb = o >> 4, m = o & 15, ob = i >> 4, g = (i >> 2) & 3, j = i & 3;
-    s_wa[((layer * 16 + ob * 4 + j) * kWave + 16 * g + m) * 4 + mb] = 4.0f * value;
-  };
-  if ((reinterpret_cast<uintptr_t>(params) & 15) == 0) {
-    f4 v[kPerThread];
+  constexpr int kItems = 3 * 4 * kWave;  // (layer, ob, lane)
+  const bool aligned = (reinterpret_cast<uintptr_t>(params) & 15) == 0;
+  f4* wa = reinterpret_cast<f4*>(s_wa);
+  for (int item = tid; item < kItems; item += kThreads) {
+    const int lane = item & (kWave - 1), ob = (item >> 6) & 3, layer = item >> 8;
+    const float* block = params + kHiddenBase + layer * kHiddenStride + (lane & 15) * kHidden +
+                         16 * ob + 4 * (lane >> 4);
+    f4 rows[4];
 #pragma unroll
-    for (int n = 0; n < kPerThread; ++n) {
-      const int q = tid + n * kThreads;
-      if (q < kQuads) {
-        const int layer = q >> 10, o = q & 63, i = ((q >> 6) & 15) << 2;
-        v[n] = *reinterpret_cast<const f4*>(params + kHiddenBase + layer * kHiddenStride + (o << 6) + i);
-      }
+    for (int mb = 0; mb < 4; ++mb) {
+      const float* p = block + 16 * kHidden * mb;
+      rows[mb] = aligned ? *reinterpret_cast<const f4*>(p) : f4{p[0], p[1], p[2], p[3]};
     }
 #pragma unroll
-    for (int n = 0; n < kPerThread; ++n) {
-      const int q = tid + n * kThreads;
-      if (q < kQuads) {
-        const int layer = q >> 10, o = q & 63, i = ((q >> 6) & 15) << 2;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) put(layer, o, i + e, v[n][e]);
-      }
-    }
-  } else {
-    for (int k = tid; k < 4 * kQuads; k += kThreads) {
-      const int layer = k >> 12, o = k & 63, i = (k >> 6) & 63;
-      put(layer, o, i, params[kHiddenBase + layer * kHiddenStride + (o << 6) + i]);
+    for (int j = 0; j < 4; ++j) {
+      wa[(16 * layer + 4 * ob + j) * kWave + lane] =
+          4.0f * f4{rows[0][j], rows[1][j], rows[2][j], rows[3][j]};
     }
   }
 }
