@@ -97,24 +97,17 @@ __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
 
 __device__ __forceinline__ f4 lds4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 
-// tanh in the scaled jet. Input zv = c z_v; outputs v = (c / 4) tanh(z_v) and
-// s = (1 - tanh^2 z_v) / 4. With t = exp(-2 z_v) = exp2(zv) and u = 1 / (1 + t):
+// tanh in the scaled jet, four values at a time. Input zv = c z_v; outputs v = (c / 4) tanh(z_v)
+// and s = (1 - tanh^2 z_v) / 4. With t = exp(-2 z_v) = exp2(zv) and u = 1 / (1 + t):
 //   tanh z_v = 2 u - 1,   1 - tanh^2 z_v = 4 u (1 - u),
 // so v = fma(u, c / 2, -c / 4) and s = fma(-u, u, u): 3 VALU + 2 transcendental instructions
-// (v_exp_f32, v_rcp_f32). t overflows to +inf for z_v < -44 (u = 0: tanh = -1, s = 0) and
-// flushes to 0 for z_v > 44 (u = 1: tanh = 1, s = 0). Near tanh = +1, s carries the absolute
-// rounding of u (about 6e-8), as 1 - a^2 does.
-__device__ __forceinline__ void tanh_scaled(float zv, float& v, float& s) {
-  const float u = __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(zv) + 1.0f);
-  v = __builtin_fmaf(u, 0.5f * kC, -0.25f * kC);
-  s = __builtin_fmaf(-u, u, u);
-}
-
-// tanh_scaled of four values, in stages across the four: the four exp2, then the four rcp, then
-// the rest, with fences so the scheduler keeps the stages. Each value's chain is serial
-// (exp2 -> add -> rcp -> fma), and left alone the compiler ran the chains one after another;
-// a wave alone on its SIMD (the backward, the forward's last tiles) then waited out every
-// transcendental's latency. Same operations per value as tanh_scaled.
+// (v_exp_f32, v_rcp_f32) per value. t overflows to +inf for z_v < -44 (u = 0: tanh = -1,
+// s = 0) and flushes to 0 for z_v > 44 (u = 1: tanh = 1, s = 0). Near tanh = +1, s carries the
+// absolute rounding of u (about 6e-8), as 1 - a^2 does.
+// The four values go in stages: the four exp2, then the four rcp, then the rest, with fences
+// so the scheduler keeps the stages. Each value's chain is serial (exp2 -> add -> rcp -> fma),
+// and left alone the compiler ran the chains one after another; a wave alone on its SIMD (the
+// backward, the forward's last tiles) then waited out every transcendental's latency.
 __device__ __forceinline__ void tanh_scaled4(const f4 zv, f4& v, f4& s) {
   f4 u;
 #pragma unroll
@@ -984,110 +977,6 @@ __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&
   dw_product(stage_rows, w, dw);
 }
 
-// ---- value channel only (boundary tiles of the fused step) ----
-// The building blocks above restricted to jet component 0, with the same operand order, so
-// each accumulator sees the same sequence of MFMAs as its component-0 counterpart.
-
-// acc[mb] = bias[mb] + W[16 mb + ., :] hv: component 0 of hidden_product.
-__device__ __forceinline__ void hidden_product_value(const float* w, const f4 (&hv)[4],
-                                                     const f4 (&bias)[4], f4 (&acc)[4]) {
-  f4 next[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) next[mb] = lds4(w + 1088 * mb);
-#pragma unroll
-  for (int ob = 0; ob < 4; ++ob) {
-    f4 a[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) a[mb] = next[mb];
-    if (ob < 3) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) next[mb] = lds4(w + 1088 * mb + 16 * (ob + 1));
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) acc[mb] = mfma(a[mb][j], hv[ob][j], (ob | j) ? acc[mb] : bias[mb]);
-    }
-    if (ob < 3) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-  }
-}
-
-// hb[ib] = sum_o W[o][16 ib + .] zb[o]: component 0 of hidden_product_t.
-__device__ __forceinline__ void hidden_product_t_value(const float* w, const f4 (&zb)[4],
-                                                       f4 (&hb)[4]) {
-  float next[4];
-#pragma unroll
-  for (int ib = 0; ib < 4; ++ib) next[ib] = w[16 * ib];
-#pragma unroll
-  for (int step = 0; step < 16; ++step) {
-    const int ob = step >> 2, j = step & 3;
-    float a[4];
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) a[ib] = next[ib];
-    if (step < 15) {
-      const int nob = (step + 1) >> 2, nj = (step + 1) & 3;
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib) next[ib] = w[1088 * nob + kWRow * nj + 16 * ib];
-    }
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      hb[ib] = mfma(a[ib], zb[ob][j], (ob | j) ? hb[ib] : f4{0.f, 0.f, 0.f, 0.f});
-    }
-    if (step < 15) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-  }
-}
-
-// dW += zbar_v h_v^T over the workgroup tile (planes 0 and 2 only: the cc = 0 half of
-// dw_product). Returns the sum of this lane's zbar_v reads.
-__device__ __forceinline__ float dw_product_value(const float* stage_rows, int w, f4 (&dw)[4]) {
-  float bias = 0.0f;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const f4 a = lds4(stage_rows + 1088 * w + 16 * s);
-    f4 b[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) b[nb] = lds4(stage_rows + 2 * kPlane + 1088 * nb + 16 * s);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      bias += a[k];
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) dw[nb] = mfma(a[k], b[nb][k], dw[nb]);
-    }
-  }
-  return bias;
-}
-
-// stage_and_dw for the value channel: stages zbar_v and the previous layer's v = tanh(zp) (or,
-// with kFromLayer0, layer 0's), accumulates dW and the bias gradient, and returns the previous
-// layer's (v', s) in (pv, ps).
-template <bool kFromLayer0>
-__device__ __forceinline__ void stage_and_dw_value(const f4 (&zbar)[4], const f4 (&zp)[4],
-                                                   f4 (&dw)[4], float& g_bias, float* stage_lane,
-                                                   const float* stage_rows, const float* s_small,
-                                                   int w, int g, float x0, float x1, f4 (&pv)[4],
-                                                   f4 (&ps)[4]) {
-  __syncthreads();  // previous readers of the staging buffer are done
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    Layer0Weights w0;
-    if (kFromLayer0) w0 = layer0_weights(s_small, mb, g);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v, sl;
-      tanh_scaled(kFromLayer0 ? layer0_zv(w0, r, x0, x1) : zp[mb][r], v, sl);
-      pv[mb][r] = v;
-      ps[mb][r] = sl;
-      float* p = stage_lane + 1088 * mb + kWRow * r;
-      p[0] = zbar[mb][r];
-      p[2 * kPlane] = v;
-    }
-  }
-  __syncthreads();
-  g_bias += sum_lane_groups(dw_product_value(stage_rows, w, dw));
-}
-
 // Seed of the fused Poisson training step (kLoss). The loss is the PINN loss
 //   mean_interior (lap - f)^2 + w mean_boundary u^2
 // (/root/reference/src/fused_hoad/training.py:66-88; with no boundary points, the loss of
@@ -1095,14 +984,15 @@ __device__ __forceinline__ void stage_and_dw_value(const f4 (&zbar)[4], const f4
 // forward, so it forms the upstream gradients autograd would form for that loss itself:
 //   interior points: grad_u = 0, grad_lap = fl(1 / B) (2 r) with r = lap - f;
 //   boundary points: grad_u = fl(w / B_b) (2 u), grad_lap = 0.
-// Tiles [0, interior_tiles) hold interior points and the rest boundary points. sum r^2 and
+// Tiles [0, interior_tiles) hold interior points and the rest boundary points, 16 per tile in
+// both gradient kernels (boundary_tile, backward_split_kernel). sum r^2 and
 // sum u^2 go into columns kLossColumn and kLossColumn + 1 of the slot's partial row. `step` is
 // the Adam step counter, advanced here (one lane of workgroup 0) so that the update kernel that
 // follows reads a settled value.
 struct LossSeed {
   const float* source;     // f[batch]
   const float* boundary;   // boundary coordinates [boundary_count][2]
-  int64_t interior_tiles;  // ceil(batch / 64)
+  int64_t interior_tiles;  // ceil(batch / 64) (backward_kernel) or ceil(batch / 16) (split)
   int64_t boundary_count;
   float inv_batch;         // fl(1 / B)
   float boundary_scale;    // fl(fl(w) / B_b)
@@ -1123,128 +1013,178 @@ struct WaveSums {
 
 // A boundary tile of the fused step. Boundary points enter the loss through u alone
 // (grad_lap = 0), so the output seed is (vbar', Jbar', Lbar') = (4 gu w_out / c, 0, 0), and the
-// tanh-jet adjoint maps (vbar, 0, 0, 0) to (s vbar, 0, 0, 0): every adjoint component but the
-// value one is exactly zero at every layer. The weight-gradient terms reduce to zbar_v h_v^T,
-// and the forward's J and L components feed nothing. This tile therefore runs the value
-// channel only, a quarter of the MFMA work of an interior tile; the terms it skips are exact
-// zeros. (The result can still differ from a full-jet run in the last bit: the full jet forms
-// some of these products as fma(a, b, 0), which the compiler cannot fuse into the row sums
-// that follow, and a plain a * b it may.)
-__device__ __forceinline__ void boundary_value_tile(const float* s_w, const float* s_small,
-                                                    float* s_stage, int rows_off, int cols_off,
-                                                    int stage_lane_off, int w, int g, int m_pick,
-                                                    float x0, float x1, bool active,
-                                                    float boundary_scale, WaveSums& acc) {
-  f4 hv[4], z1[4], z2[4], z3[4], bias[4];
+// tanh-jet adjoint maps (vbar', 0, 0, 0) to (s' vbar', 0, 0, 0): every adjoint component but
+// the value one is exactly zero at every layer. The weight-gradient terms reduce to
+// zbar_v h_v^T, and the forward's J and L components feed nothing. A boundary tile therefore
+// runs the value channel only; the terms it skips are exact zeros.
+//
+// A boundary tile holds 16 points, shared by the workgroup's 4 waves: wave w owns rows
+// 16 w .. 16 w + 15 of every layer, so the forward, dW and W^T zbar products of a layer are 16
+// MFMAs each per wave (a 16-point value-channel tile on one wave would be 64 each). Layer
+// outputs and adjoints go to the other waves lane to lane through LDS (the register layout of
+// forward_split_kernel: register r of block ob holds row 16 ob + 4 g + r at point m), for the
+// next product's B operand. dW contracts over the tile's points, which sit on the lane axis, so
+// each layer's h_v and the wave's zbar_v are also stored transposed: row R, point 4 s + g at
+// column 4 g + s of a 20-float row, so one 16-byte read gives a lane the points of its 4 k-steps.
+// Scratch inside the dW staging buffer (floats):
+constexpr int kBndPitch = 20;                                   // transposed row, 16 points + pad
+constexpr int kBndExchange = 0;                                 // [2][4 waves][64 lanes] f4
+constexpr int kBndH = kBndExchange + 2 * kBwdWaves * kWave * 4;  // [3 layers][64 rows][pitch]
+constexpr int kBndZ = kBndH + 3 * kHidden * kBndPitch;          // [2][4 waves][16 rows][pitch]
+static_assert(kBndZ + 2 * kBwdWaves * 16 * kBndPitch <= 4 * kPlane,
+              "the boundary tile's scratch must fit the dW staging buffer");
+
+// Store this lane's 4 rows row0 + 4 g + r (value at point m) into a transposed buffer.
+__device__ __forceinline__ void store_point_columns(float* t, int row0, int g, int m, f4 x) {
+  const int col = 4 * (m & 3) + (m >> 2);
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const Layer0Weights w0 = layer0_weights(s_small, mb, g);
+  for (int r = 0; r < 4; ++r) t[(row0 + 4 * g + r) * kBndPitch + col] = x[r];
+}
+
+// Per-neuron point sums of this wave's rows: t[r] is the total of row 16 w + 4 g + r (the same
+// in all 16 lanes of row g). Lane (m, g) owns neuron owned_neuron(m, g) =
+// 16 (m >> 2) + 4 g + (m & 3) in the slot sums, so it takes t[m & 3] when m >> 2 == w and adds
+// nothing otherwise (the other waves own those neurons' rows).
+__device__ __forceinline__ float own_row_total(const f4 t, int m, int w) {
+  const float lo = (m & 1) ? t[1] : t[0];
+  const float hi = (m & 1) ? t[3] : t[2];
+  const float v = (m & 2) ? hi : lo;
+  return (m >> 2) == w ? v : 0.0f;
+}
+
+__device__ __forceinline__ f4 row_totals(const f4 x) {
+  f4 t;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v, s;
-      tanh_scaled(layer0_zv(w0, r, x0, x1), v, s);
-      hv[mb][r] = v;
-    }
+  for (int r = 0; r < 4; ++r) t[r] = sum_row16(x[r]);
+  return t;
+}
+
+__device__ __forceinline__ void boundary_tile(const float* s_w, const float* s_small,
+                                              float* s_stage, int rows_off, int cols_off, int w,
+                                              int g, int m, float x0, float x1, bool active,
+                                              float boundary_scale, WaveSums& acc) {
+  __syncthreads();  // the previous tile's readers of the staging buffer are done
+  f4* xch = reinterpret_cast<f4*>(s_stage + kBndExchange);
+  float* ht = s_stage + kBndH;
+  float* zt = s_stage + kBndZ;
+  const int lane = 16 * g + m;
+  int phase = 0;  // alternates the exchange and zbar buffers
+
+  // ---- forward, value channel: layer 0 whole, then this wave's rows of hidden layers 1..3 ----
+  f4 h[4];      // v' of all 64 rows of the current layer output
+  f4 s_own[3];  // s' of this wave's rows of layer 0 and hidden layers 1, 2
+  f4 v_top, s_top;  // hidden layer 3, this wave's rows
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) {
+    const Layer0Weights w0 = layer0_weights(s_small, ob, g);
+    f4 zv, unused;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) zv[r] = layer0_zv(w0, r, x0, x1);
+    tanh_scaled4(zv, h[ob], unused);
   }
-  load_bias(s_small, 0, g, bias);
-  hidden_product_value(s_w + opaque(rows_off), hv, bias, z1);
+  {
+    // this wave's block again (h[w] would need a dynamic register index)
+    const Layer0Weights w0 = layer0_weights(s_small, w, g);
+    f4 zv, v;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v, s;
-      tanh_scaled(z1[mb][r], v, s);
-      hv[mb][r] = v;
-    }
+    for (int r = 0; r < 4; ++r) zv[r] = layer0_zv(w0, r, x0, x1);
+    tanh_scaled4(zv, v, s_own[0]);
+    store_point_columns(ht, 16 * w, g, m, v);
   }
-  load_bias(s_small, 1, g, bias);
-  hidden_product_value(s_w + opaque(rows_off) + kPlane, hv, bias, z2);
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
+  for (int l = 0; l < 3; ++l) {
+    const f4 b = lds4(s_small + kSmallBh + l * kHidden + 16 * w + 4 * g);
+    const float* wrow = s_w + l * kPlane + opaque(rows_off) + 1088 * w;  // W[16 w + m][.]
+    f4 z;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v, s;
-      tanh_scaled(z2[mb][r], v, s);
-      hv[mb][r] = v;
+    for (int ob = 0; ob < 4; ++ob) {
+      const f4 a = lds4(wrow + 16 * ob);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) z = mfma(a[j], h[ob][j], (ob | j) ? z : b);
     }
-  }
-  load_bias(s_small, 2, g, bias);
-  hidden_product_value(s_w + opaque(rows_off) + 2 * kPlane, hv, bias, z3);
-  f4 tv[4], ts[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v, s;
-      tanh_scaled(z3[mb][r], v, s);
-      tv[mb][r] = v;
-      ts[mb][r] = s;
+    f4 v, sl;
+    tanh_scaled4(z, v, sl);
+    if (l < 2) {
+      s_own[l + 1] = sl;
+      store_point_columns(ht + (l + 1) * kHidden * kBndPitch, 16 * w, g, m, v);
+    } else {
+      v_top = v;
+      s_top = sl;
     }
+    xch[(phase * kBwdWaves + w) * kWave + lane] = v;
+    __syncthreads();
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) h[ob] = xch[(phase * kBwdWaves + ob) * kWave + lane];
+    phase ^= 1;
   }
 
-  // u = w_out . v + b_out, the seed gu = fl(w / B_b) (2 u), and the output-layer sums.
+  // ---- u = w_out . v + b_out over all 64 rows, the seed gu = fl(w / B_b) (2 u) ----
   float out = 0.0f;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const f4 wo = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+  for (int ob = 0; ob < 4; ++ob) {
+    const f4 wo = lds4(s_small + kSmallWoutV + 16 * ob + 4 * g);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) out = __builtin_fmaf(wo[r], tv[mb][r], out);
+    for (int r = 0; r < 4; ++r) out = __builtin_fmaf(wo[r], h[ob][r], out);
   }
   out = sum_lane_groups(out);
   const float u = active ? out + s_small[kSmallBout] : 0.0f;
   const float gu = boundary_scale * (2.0f * u);
-  acc.bloss += sum_row16(u * u);
-  const float gu_c = gu * (4.0f / kC);
-  f4 zb[4], hb[4];
-  {
-    float wout_terms[16];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        wout_terms[4 * mb + r] = gu_c * tv[mb][r];
-        zb[mb][r] = ts[mb][r] * (gu * wv[r]);  // hidden layer 3's zbar_v = s vbar
-      }
-    }
-    acc.wout += row_reduce_scatter16(wout_terms, m_pick);
+  if (w == 0) {  // the 4 waves share the tile's points: one of them adds the point sums
+    acc.bloss += sum_row16(u * u);
     acc.bout += sum_row16(gu);
   }
+  const float gu_c = gu * (4.0f / kC);
+  acc.wout += own_row_total(row_totals(gu_c * v_top), m, w);
+  const f4 wv = lds4(s_small + kSmallWoutV + 16 * w + 4 * g);
+  f4 zb = s_top * (gu * wv);  // hidden layer 3's zbar_v' = s' vbar', this wave's rows
 
-  // Hidden layers 3, 2, 1: dW, then hbar_v = W^T zbar_v and the next zbar_v = s hbar_v.
-  stage_and_dw_value<false>(zb, z2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
-                            s_stage + opaque(rows_off), s_small, w, g, x0, x1, tv, ts);
-  hidden_product_t_value(s_w + opaque(cols_off) + 2 * kPlane, zb, hb);
+  // ---- hidden layers 3, 2, 1: dW, the bias sum, hbar = W^T zbar, the next zbar ----
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) zb[mb] = ts[mb] * hb[mb];
-  stage_and_dw_value<false>(zb, z1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
-                            s_stage + opaque(rows_off), s_small, w, g, x0, x1, tv, ts);
-  hidden_product_t_value(s_w + opaque(cols_off) + kPlane, zb, hb);
+  for (int l = 2; l >= 0; --l) {
+    float* ztw = zt + (phase * kBwdWaves + w) * 16 * kBndPitch;
+    store_point_columns(ztw, 0, g, m, zb);
+    xch[(phase * kBwdWaves + w) * kWave + lane] = zb;
+    __syncthreads();
+    {
+      // dW[16 w + ., 16 nb + .] += sum over the 16 points of zbar h_prev^T: A = zbar of row
+      // 16 w + m, B = h_prev of row 16 nb + m, k-step s = points 4 s + g.
+      const f4 a = lds4(ztw + m * kBndPitch + 4 * g);
+      const float* hrow = ht + l * kHidden * kBndPitch + m * kBndPitch + 4 * g;
+      f4 bt[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) zb[mb] = ts[mb] * hb[mb];
-  stage_and_dw_value<true>(zb, z1, acc.dw[0], acc.bh[0], s_stage + opaque(stage_lane_off),
-                           s_stage + opaque(rows_off), s_small, w, g, x0, x1, tv, ts);
-  hidden_product_t_value(s_w + opaque(cols_off), zb, hb);
-
-  // Layer 0: bv = s' hbar_v'; dW0[o][d] = 2 sum_p bv (c x_d / 2) (the row takes the 2),
-  // db0 = c sum_p bv.
-  {
-    float tx[16], ty[16], tb[16];
-    const float cx0 = kHalfC * x0, cx1 = kHalfC * x1;
+      for (int nb = 0; nb < 4; ++nb) bt[nb] = lds4(hrow + 16 * nb * kBndPitch);
+      float bsum = 0.0f;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+      for (int k = 0; k < 4; ++k) {
+        bsum += a[k];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float bv = ts[mb][r] * hb[mb][r];
-        tx[4 * mb + r] = bv * cx0;
-        ty[4 * mb + r] = bv * cx1;
-        tb[4 * mb + r] = bv;
+        for (int nb = 0; nb < 4; ++nb) acc.dw[l][nb] = mfma(a[k], bt[nb][k], acc.dw[l][nb]);
+      }
+      acc.bh[l] += sum_lane_groups(bsum);
+    }
+    f4 hb;
+    {
+      // hbar of this wave's rows of the layer below: sum over the 64 rows o of
+      // W[o][16 w + m] zbar[o].
+      const float* wt = s_w + l * kPlane + opaque(cols_off) + 16 * w;
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) {
+        const f4 zo = xch[(phase * kBwdWaves + ob) * kWave + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          hb = mfma(wt[1088 * ob + kWRow * j], zo[j], (ob | j) ? hb : zero4());
+        }
       }
     }
-    acc.w0x += row_reduce_scatter16(tx, m_pick);
-    acc.w0y += row_reduce_scatter16(ty, m_pick);
-    acc.b0 += row_reduce_scatter16(tb, m_pick);
+    phase ^= 1;
+    zb = s_own[l] * hb;  // zbar_v' of the layer below (l = 0: layer 0's bv)
   }
+
+  // ---- layer 0: dW0[o][d] = 2 sum_p bv (c x_d / 2) (the row takes the 2), db0 = c sum_p bv ----
+  const float cx0 = kHalfC * x0, cx1 = kHalfC * x1;
+  acc.w0x += own_row_total(row_totals(zb * cx0), m, w);
+  acc.w0y += own_row_total(row_totals(zb * cx1), m, w);
+  acc.b0 += own_row_total(row_totals(zb), m, w);
 }
 
 // Per-point inputs of one gradient-kernel tile for this lane: coordinates and, for interior
@@ -1261,8 +1201,8 @@ __device__ __forceinline__ TileInputs load_tile_inputs(const float* __restrict__
                                                        int64_t batch, const LossSeed& seed,
                                                        int64_t tile, int w, int m) {
   TileInputs in{0.f, 0.f, 0.f, 0.f};
-  if (kLoss && tile >= seed.interior_tiles) {
-    const int64_t point = (tile - seed.interior_tiles) * kBwdTile + kTile * w + m;
+  if (kLoss && tile >= seed.interior_tiles) {  // 16-point boundary tile, shared by the waves
+    const int64_t point = (tile - seed.interior_tiles) * kTile + m;
     if (point < seed.boundary_count) {
       in.x0 = seed.boundary[2 * point];
       in.x1 = seed.boundary[2 * point + 1];
@@ -1509,10 +1449,10 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
           next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed,
                                          tile + slots, w, m);
         }
-        const int64_t point = (tile - seed.interior_tiles) * kBwdTile + kTile * w + m;
+        const int64_t point = (tile - seed.interior_tiles) * kTile + m;
         const bool active = point < seed.boundary_count;
-        boundary_value_tile(s_w, s_small, s_stage, rows_off, cols_off, stage_lane_off, w, g,
-                            m_pick, in.x0, in.x1, active, seed.boundary_scale, acc);
+        boundary_tile(s_w, s_small, s_stage, rows_off, cols_off, w, g, m_pick, in.x0, in.x1,
+                      active, seed.boundary_scale, acc);
         deliver(next);
       }
     }
@@ -2070,7 +2010,7 @@ bool use_split_backward(int64_t batch, int64_t boundary_count) {
 // stashes) and backward_split_kernel's (partial rows).
 size_t gradient_workspace_bytes(int64_t batch, int64_t boundary_count) {
   const size_t tiled = workspace_bytes_for(
-      slots_for_tiles(backward_tiles(batch) + backward_tiles(boundary_count)));
+      slots_for_tiles(backward_tiles(batch) + split_tiles(boundary_count)));
   const size_t split =
       static_cast<size_t>(slots_for_tiles(split_tiles(batch) + split_tiles(boundary_count))) *
       kRowStride * sizeof(float);
@@ -2240,8 +2180,7 @@ extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* so
   if (int st = check_workspace_alignment(workspace)) return st;
   const bool split = use_split_backward(batch, boundary_count);
   const int64_t interior_tiles = split ? split_tiles(batch) : backward_tiles(batch);
-  const int64_t tiles =
-      interior_tiles + (split ? split_tiles(boundary_count) : backward_tiles(boundary_count));
+  const int64_t tiles = interior_tiles + split_tiles(boundary_count);  // 16-point boundary tiles
   const int slots = slots_for_tiles(tiles);
   int grid = 0;
   if (int st = backward_grid(slots, &grid)) return st;

@@ -79,10 +79,11 @@ def test_constants_and_status_strings() -> None:
 
 def _expected_workspace(batch: int, boundary: int = 0) -> int:
     """Either gradient kernel may run (a knob can force either), so the workspace covers the
-    larger need: 64-point tiles with a partial row and four 16 KB wave stashes per slot, or
-    16-point tiles with a partial row per slot; at most 256 slots."""
+    larger need: 64-point interior tiles and 16-point boundary tiles with a partial row and
+    four 16 KB wave stashes per slot, or 16-point tiles with a partial row per slot; at most
+    256 slots."""
     row = 12800 * 4
-    tiled = min(256, -(-batch // 64) - (-boundary // 64)) * (row + 4 * 16 * 1024)
+    tiled = min(256, -(-batch // 64) - (-boundary // 16)) * (row + 4 * 16 * 1024)
     split = min(256, -(-batch // 16) - (-boundary // 16)) * row
     return max(tiled, split)
 
