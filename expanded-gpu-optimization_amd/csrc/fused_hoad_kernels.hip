@@ -319,7 +319,7 @@ __device__ __forceinline__ void stage_operand_weights(const float* __restrict__ 
 // Layer-0 data of the 4 neurons o = 16 mb + 4 g + r (r = 0..3) held by this lane.
 struct Layer0Weights {
   f4 cwx, cwy, cb;  // scaled, for the pre-activation c z_v = c (W0 x + b0)
-  f4 wx, wy, q;     // z_J0, z_J1 of layer 0 (the W0 columns) and their squared norm
+  f4 wx, wy, q;     // z'_J0, z'_J1 of layer 0 (2 x the W0 columns) and their squared norm
 };
 
 __device__ __forceinline__ Layer0Weights layer0_weights(const float* s_small, int mb, int g) {
@@ -473,7 +473,7 @@ __device__ __forceinline__ void apply_tanh_jet(const f4 (&z)[4][4], f4 (&h)[4][4
   }
 }
 
-// apply_tanh_jet that also returns (v', s) of every value.
+// apply_tanh_jet that also returns (v', s') of every value.
 __device__ __forceinline__ void apply_tanh_jet_vs(const f4 (&z)[4][4], f4 (&h)[4][4],
                                                   f4 (&tv)[4], f4 (&ts)[4]) {
 #pragma unroll
@@ -906,7 +906,7 @@ __device__ __forceinline__ void tanh_adjoint_seed_in_place(f4 (&z)[4][4], const 
 }
 
 // Replace a hidden layer's pre-activation z by its adjoint zbar, given the adjoint hb of the
-// layer's output and the layer's (v', s) from tanh_scaled (lane-local).
+// layer's output and the layer's (v', s') from tanh_scaled4 (lane-local).
 __device__ __forceinline__ void tanh_adjoint_in_place(f4 (&z)[4][4], const f4 (&hb)[4][4],
                                                       const f4 (&tv)[4], const f4 (&ts)[4]) {
 #pragma unroll
@@ -925,11 +925,11 @@ __device__ __forceinline__ void tanh_adjoint_in_place(f4 (&z)[4][4], const f4 (&
 }
 
 // dW += zbar h_prev^T over the workgroup tile, in two passes of two jet components: (v, L)
-// first, then (J0, J1). h_prev = tanh_jet(zp) is rebuilt from the previous layer's
-// pre-activation (or, with kFromLayer0, from layer 0's closed form
-// z = (c (W0 x + b0), W0[:,0], W0[:,1], 0)); one tanh per value serves both passes, and its
-// (v', s) are returned in (pv, ps) for the previous layer's own adjoint. Adds the bias
-// gradient sum_p zbar_v / c to g_bias.
+// first, then (J0, J1). h_prev, the tanh jet of zp, is rebuilt from the previous layer's
+// scaled pre-activation (or, with kFromLayer0, from layer 0's closed form
+// z' = (c (W0 x + b0), 2 W0[:,0], 2 W0[:,1], 0)); one tanh per value serves both passes, and
+// its (v', s') are returned in (pv, ps) for the previous layer's own adjoint. Adds the bias
+// gradient sum_p zbar_v' = sum_p zbar_v / c to g_bias.
 template <bool kFromLayer0>
 __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&zp)[4][4],
                                              f4 (&dw)[4], float& g_bias, float* stage_lane,
@@ -1329,7 +1329,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       hidden_layer(s_small, s_w + opaque(rows_off), 1, g, h, z2);
       apply_tanh_jet(z2, h);
       hidden_layer(s_small, s_w + opaque(rows_off), 2, g, h, z3);
-      f4 tv[4], ts[4];  // (v', s) of the layer whose adjoint comes next
+      f4 tv[4], ts[4];  // (v', s') of the layer whose adjoint comes next
       apply_tanh_jet_vs(z3, h, tv, ts);
 
       if (kLoss) {
