@@ -10,7 +10,10 @@ separate small calls on the same points:
 * the backward gets upstream gradients that are zero except at three points past 2^31 (in
   three different slots), so its parameter gradient is those three points' gradient, summed in
   another order than the small call sums it (1e-5 of each block's scale), and its coordinate
-  gradient is zero everywhere else.
+  gradient is zero everywhere else;
+* the fused training step (lr 0, so the weights stay put) with a random source term: its loss
+  against a float64 sum of (lap - f)^2 over the forward's Laplacian, and its gradient against
+  the backward call seeded with grad_lap = 2 (lap - f) / B (the same tiles and slots).
 """
 
 from __future__ import annotations
@@ -86,4 +89,36 @@ def test_backward_past_two_to_the_31_points() -> None:
     assert_scaled_close(gx[idx], sx, 1e-5, "grad_coordinates at the seeded points")
     assert int(torch.count_nonzero(gx)) <= 6, "grad_coordinates must be zero at unseeded points"
     del x, gu, gl, gx
+    torch.cuda.empty_cache()
+
+
+def test_fused_step_past_two_to_the_31_points() -> None:
+    from fused_hoad import DEFAULT_POISSON_MLP, build_mlp
+    from fused_hoad._extension import fused_forward_laplacian, fused_forward_laplacian_backward
+    from fused_hoad.training import FusedPoissonAdam
+
+    announce(f"fused step, batch={BIG} (2^31 + 4099), random source, lr 0")
+    x = _big_coordinates()
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    f = torch.rand(BIG, device="cuda", generator=gen)
+    torch.manual_seed(0)
+    model = build_mlp(DEFAULT_POISSON_MLP).cuda()
+    trainer = FusedPoissonAdam(model, x, f, lr=0.0)
+    p = trainer.parameters.clone()
+    loss = float(trainer.step())
+    assert torch.equal(trainer.parameters, p), "lr 0 must leave the parameters unchanged"
+    _, lap = fused_forward_laplacian(x, p)
+    lap = lap.reshape(-1)
+    want = 0.0
+    for lo in range(0, BIG, 1 << 28):
+        r = lap[lo : lo + (1 << 28)].double() - f[lo : lo + (1 << 28)].double()
+        want += float((r * r).sum())
+    want /= BIG
+    assert abs(loss - want) <= 1e-4 * want, f"loss {loss} vs {want}"
+    gl = (lap - f) * (2.0 / BIG)
+    del lap
+    gp, _ = fused_forward_laplacian_backward(x, p, torch.zeros_like(gl), gl)
+    for name, lo, hi in BLOCKS:
+        assert_scaled_close(trainer.grad[lo:hi], gp[lo:hi], 1e-6, name)
+    del x, f, trainer, gl, gp
     torch.cuda.empty_cache()
