@@ -1194,12 +1194,13 @@ struct TileInputs {
   float x0, x1, a, b;
 };
 
-template <bool kLoss>
+template <bool kLoss, bool kRest = false>
 __device__ __forceinline__ TileInputs load_tile_inputs(const float* __restrict__ coordinates,
                                                        const float* __restrict__ grad_output,
                                                        const float* __restrict__ grad_laplacian,
-                                                       int64_t batch, const LossSeed& seed,
-                                                       int64_t tile, int w, int m) {
+                                                       int64_t batch, int64_t whole,
+                                                       const LossSeed& seed, int64_t tile, int w,
+                                                       int m) {
   TileInputs in{0.f, 0.f, 0.f, 0.f};
   if (kLoss && tile >= seed.interior_tiles) {  // 16-point boundary tile, shared by the waves
     const int64_t point = (tile - seed.interior_tiles) * kTile + m;
@@ -1209,7 +1210,9 @@ __device__ __forceinline__ TileInputs load_tile_inputs(const float* __restrict__
     }
     return in;
   }
-  const int64_t point = tile * kBwdTile + kTile * w + m;
+  // 64-point tiles below `whole`, then (kRest) 16-point tiles shared by the waves (split_tile).
+  const int64_t point = !kRest || tile < whole ? tile * kBwdTile + kTile * w + m
+                                               : whole * kBwdTile + (tile - whole) * kTile + m;
   if (point < batch) {
     in.x0 = coordinates[2 * point];
     in.x1 = coordinates[2 * point + 1];
@@ -1231,6 +1234,243 @@ __device__ __forceinline__ void deliver(TileInputs& in) {
   in.b = opaque(in.b);
 }
 
+constexpr int kSplitBwdMaxTiles = 768;  // backward_split_kernel up to 768 16-point tiles
+constexpr int kTPlane = 64 * kWRow;     // floats of one transposed 64-row layer (h)
+constexpr int kTWave = 16 * kWRow;      // floats of one wave's transposed zbar
+
+// Store this lane's 4 rows (rows0 + 4 g + r) x 4 components at point m into a transposed
+// buffer t[row][68]: component c of point p = 4 s + g' at t[row * 68 + 16 c + 4 g' + s].
+__device__ __forceinline__ void store_transposed(float* t, int rows0, int g, int m,
+                                                 const f4 (&x)[4]) {
+  const int col = 4 * (m & 3) + (m >> 2);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) t[(rows0 + 4 * g + r) * kWRow + 16 * c + col] = x[c][r];
+  }
+}
+
+// Scratch of one 16-point tile whose rows are split over the workgroup's 4 waves.
+struct SplitScratch {
+  float* ht;                       // [3][kTPlane]: h of layers 0..2, transposed
+  f4 (*x)[kSplitWaves][4][kWave];  // [2 buffers]: lane-major exchange
+  float (*zt)[kTWave];             // [4 waves]: this wave's zbar, transposed
+  float (*gx)[2][kTile];           // [4 waves]: partial coordinate gradients
+};
+constexpr int kSplitScratchFloats = 3 * kTPlane + 2 * kSplitWaves * 4 * kWave * 4 +
+                                    kSplitWaves * kTWave + kSplitWaves * 2 * kTile;
+
+// Per-lane point sums of split_tile: bias sums go to the caller's array (row 16 w + m, as in
+// dw_product); these are of row 16 w + 4 g + (m & 3) (w0x, w0y, b0, wout), or the same in every
+// lane of a wave (bout, loss, bloss).
+struct SplitSums {
+  float w0x, w0y, b0, wout, bout, loss, bloss;
+};
+
+// One 16-point tile, all 4 waves: wave w owns rows 16 w .. 16 w + 15 of every layer (64 MFMAs
+// per layer for the forward re-run, dW and W^T zbar). Layer outputs and adjoints go to the
+// other waves lane to lane through LDS (`sc.x`, the register layout of forward_split_kernel),
+// and each layer's h (all 64 rows) and the wave's zbar are also stored transposed,
+// [row][c][4 g + s] for point 4 s + g at pitch 68, so dW contracts over the tile's points with
+// 16-byte reads. dW and the bias sums accumulate into `dw` / `bias` (the layout of
+// backward_kernel's); grad_coordinates of interior points are written here. `rows_off` and
+// `cols_off` are this wave's lane offsets W[16 w + m][.] and W[.][16 w + m]; t_read = 68 m + 4 g.
+template <bool kLoss>
+__device__ __forceinline__ void split_tile(const float* s_w, const float* s_small,
+                                           const SplitScratch& sc, int& phase, int w, int g, int m,
+                                           int rows_off, int cols_off, int t_read, float x0,
+                                           float x1, float gu, float gl, float f, bool active,
+                                           bool on_boundary, int64_t point,
+                                           float* __restrict__ grad_coordinates,
+                                           const LossSeed& seed, f4 (&dw)[3][4], float (&bias)[3],
+                                           SplitSums& sums) {
+  const int lane = 16 * g + m;
+  // ---- forward re-run: all 64 rows of layer 0, then this wave's rows of layers 1..3 ----
+  f4 h[4][4];
+  layer0_forward(s_small, g, x0, x1, h);
+  {
+    f4 own[4];  // this wave's block again (h[w] would need a dynamic register index)
+    layer0_block(s_small, w, g, x0, x1, own);
+    store_transposed(sc.ht, 16 * w, g, m, own);
+  }
+  f4 z[3][4];  // this wave's pre-activations of hidden layers 1..3
+  f4 mine[4];  // this wave's rows of the current layer output
+#pragma unroll
+  for (int layer = 0; layer < 3; ++layer) {
+    const f4 b = lds4(s_small + kSmallBh + layer * kHidden + 16 * w + 4 * g);
+    const float* wrow = s_w + layer * kPlane + opaque(rows_off);
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) {
+      const f4 a = lds4(wrow + 16 * ob);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f4 cin = (ob | j) ? z[layer][c] : (c == 0 ? b : zero4());
+          z[layer][c] = mfma(a[j], h[ob][c][j], cin);
+        }
+      }
+    }
+    tanh_jet4(z[layer], mine);
+    f4 (*xb)[4][kWave] = sc.x[phase];
+    phase ^= 1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xb[w][c][lane] = mine[c];
+    if (layer < 2) store_transposed(sc.ht + (layer + 1) * kTPlane, 16 * w, g, m, mine);
+    __syncthreads();
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) h[ob][c] = xb[ob][c][lane];  // this wave's block included
+    }
+  }
+
+  if (kLoss) {
+    // u (boundary) or lap (interior) over all 64 rows, in backward_kernel's order.
+    float out = 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const f4 wo = lds4(s_small + (on_boundary ? kSmallWoutV : kSmallWoutL) + 16 * mb + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        out = __builtin_fmaf(wo[r], on_boundary ? h[mb][0][r] : h[mb][3][r], out);
+      }
+    }
+    out = sum_lane_groups(out);
+    // u (boundary) or the residual lap - f (interior); both sums are updated with a select, so
+    // that `sums` stays in registers (a branch per field made the compiler address it).
+    const float e = active ? (on_boundary ? out + s_small[kSmallBout] : out - f) : 0.0f;
+    if (on_boundary) {
+      gu = seed.boundary_scale * (2.0f * e);
+    } else {
+      gl = seed.inv_batch * (2.0f * e);
+    }
+    const float sq = sum_row16(e * e);
+    sums.bloss += on_boundary ? sq : 0.0f;
+    sums.loss += on_boundary ? 0.0f : sq;
+  }
+
+  // ---- output layer: this wave's rows of the seed and of dw_out ----
+  f4 hb[4];
+  {
+    const float gu_c = gu * (4.0f / kC);
+    const float gl_l = gl * (4.0f / kLambda);
+    const f4 wv = lds4(s_small + kSmallWoutV + 16 * w + 4 * g);
+    const f4 wl = lds4(s_small + kSmallWoutL + 16 * w + 4 * g);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float total = sum_row16(__builtin_fmaf(gu_c, mine[0][r], gl_l * mine[3][r]));
+      sums.wout = (m & 3) == r ? sums.wout + total : sums.wout;
+      hb[0][r] = gu * wv[r];
+      hb[1][r] = 0.0f;
+      hb[2][r] = 0.0f;
+      hb[3][r] = gl * wl[r];
+    }
+    sums.bout += sum_row16(gu);
+  }
+
+  // ---- hidden layers 3, 2, 1 ----
+#pragma unroll
+  for (int layer = 2; layer >= 0; --layer) {
+    // zbar of this wave's rows (tanh-jet adjoint, lane-local)
+    f4 zb[4];
+    f4 v4, s4;
+    tanh_scaled4(z[layer][0], v4, s4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = v4[r], s = s4[r];
+      float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
+      tanh_jet_adjoint_vs(v, s, z[layer][1][r], z[layer][2][r], z[layer][3][r], bv, bj0, bj1,
+                          bl);
+      zb[0][r] = bv;
+      zb[1][r] = bj0;
+      zb[2][r] = bj1;
+      zb[3][r] = bl;
+    }
+    f4 (*xb)[4][kWave] = sc.x[phase];
+    phase ^= 1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xb[w][c][lane] = zb[c];
+    float* zt = sc.zt[w];
+    store_transposed(zt, 0, g, m, zb);
+    __syncthreads();
+    // dW[16 w + ., 16 nb + .] += sum over (c, points) of zbar h_prev^T; the A reads of
+    // component 0 also give the bias sum of row 16 w + m.
+    {
+      const float* ht = sc.ht + layer * kTPlane + opaque(t_read);
+      const float* za = zt + opaque(t_read);
+      float bsum = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f4 a = lds4(za + 16 * c);
+        f4 bt[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) bt[nb] = lds4(ht + 16 * kWRow * nb + 16 * c);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          if (c == 0) bsum += a[s];
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) dw[layer][nb] = mfma(a[s], bt[nb][s], dw[layer][nb]);
+        }
+      }
+      bias[layer] += sum_lane_groups(bsum);
+    }
+    // hbar of this wave's rows of the layer below: sum over all 64 rows o of
+    // W[o][16 w + .] zbar[o].
+    {
+      const float* wt = s_w + layer * kPlane + opaque(cols_off);
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) {
+        f4 zo[4];  // zbar of rows 16 ob .. 16 ob + 15 (this wave's block included)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) zo[c] = xb[ob][c][lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = wt[1088 * ob + kWRow * j];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) hb[c] = mfma(a, zo[c][j], (ob | j) ? hb[c] : zero4());
+        }
+      }
+    }
+  }
+
+  // ---- layer 0 for this wave's rows: dW0, db0 and this wave's part of grad_x ----
+  {
+    const Layer0Weights w0 = layer0_weights(s_small, w, g);
+    const float cx0 = kHalfC * x0, cx1 = kHalfC * x1;
+    float gx0 = 0.f, gx1 = 0.f;
+    f4 zv4, v4, s4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) zv4[r] = layer0_zv(w0, r, x0, x1);
+    tanh_scaled4(zv4, v4, s4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float v = v4[r], s = s4[r];
+      float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
+      tanh_jet_adjoint_vs(v, s, w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
+      gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
+      gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
+      const float t0 = sum_row16(__builtin_fmaf(bv, cx0, bj0));
+      const float t1 = sum_row16(__builtin_fmaf(bv, cx1, bj1));
+      const float tb = sum_row16(bv);
+      sums.w0x = (m & 3) == r ? sums.w0x + t0 : sums.w0x;
+      sums.w0y = (m & 3) == r ? sums.w0y + t1 : sums.w0y;
+      sums.b0 = (m & 3) == r ? sums.b0 + tb : sums.b0;
+    }
+    gx0 = sum_lane_groups(gx0);
+    gx1 = sum_lane_groups(gx1);
+    if (g == 0) {
+      sc.gx[w][0][m] = gx0;
+      sc.gx[w][1][m] = gx1;
+    }
+    __syncthreads();
+    if (w == 0 && g == 0 && active && (!kLoss || (grad_coordinates != nullptr && !on_boundary))) {
+      grad_coordinates[2 * point] = ((sc.gx[0][0][m] + sc.gx[1][0][m]) + sc.gx[2][0][m]) + sc.gx[3][0][m];
+      grad_coordinates[2 * point + 1] = ((sc.gx[0][1][m] + sc.gx[1][1][m]) + sc.gx[2][1][m]) + sc.gx[3][1][m];
+    }
+  }
+}
+
 // z of hidden layers 2 and 3 stays in registers through the walk back; z of hidden layer 1
 // would push the live state past the register file, so each wave parks it in its own 16 KB
 // of the workspace (`stash`, coalesced 16-byte stores, L2-resident) and reloads it after
@@ -1238,15 +1478,18 @@ __device__ __forceinline__ void deliver(TileInputs& in) {
 //
 // kLoss: grad_output and grad_laplacian are unused and the seed comes from `seed` (above);
 // grad_coordinates may be null.
-template <bool kLoss>
+template <bool kLoss, bool kRest>
 __global__ void __launch_bounds__(kBwdWaves * kWave, 1)
 backward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                 const float* __restrict__ grad_output, const float* __restrict__ grad_laplacian,
                 float* __restrict__ grad_coordinates, float* __restrict__ partials,
-                f4* __restrict__ stash, int64_t batch, int64_t tiles, int slots, LossSeed seed) {
+                f4* __restrict__ stash, int64_t batch, int64_t whole, int64_t tiles, int slots,
+                LossSeed seed) {
+  constexpr int kStageFloats =
+      kRest && kSplitScratchFloats > 4 * kPlane ? kSplitScratchFloats : 4 * kPlane;
   __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
-  __shared__ __attribute__((aligned(16))) float s_stage[4 * kPlane];
+  __shared__ __attribute__((aligned(16))) float s_stage[kStageFloats];
   __shared__ float s_red[3][kBwdWaves];
   if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] += 1.0f;
   const int lane = threadIdx.x & (kWave - 1);
@@ -1256,7 +1499,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   // The first slot's first tile inputs are read before the staging, which hides their latency.
   TileInputs next{0.f, 0.f, 0.f, 0.f};
   if (static_cast<int>(blockIdx.x) < slots) {
-    next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed,
+    next = load_tile_inputs<kLoss, kRest>(coordinates, grad_output, grad_laplacian, batch, whole, seed,
                                    blockIdx.x, w, m);
   }
   stage_parameters<kBwdWaves * kWave>(params, s_w, s_small, threadIdx.x);
@@ -1287,7 +1530,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     // delivery sits before the tile's own stores, which a wait at the next tile's head would
     // also have to wait for (they are behind branches, so the compiler cannot count them).
     if (slot != static_cast<int>(blockIdx.x)) {
-      next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed, slot,
+      next = load_tile_inputs<kLoss, kRest>(coordinates, grad_output, grad_laplacian, batch, whole, seed, slot,
                                      w, m);
     }
     deliver(next);
@@ -1296,12 +1539,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     // copies a tile, where the two paths' accumulators met at the loop's back edge.
     int64_t tile = slot;
     const int64_t interior_end = kLoss ? std::min<int64_t>(tiles, seed.interior_tiles) : tiles;
-    for (; tile < interior_end; tile += slots) {
+    for (; tile < (kRest ? whole : interior_end); tile += slots) {
       keep_lds_reads_in_loop();
       const int m_pick = opaque(m);  // row_reduce_scatter16's lane masks stay inside the tile
       const TileInputs in = next;
       if (tile + slots < tiles) {
-        next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed,
+        next = load_tile_inputs<kLoss, kRest>(coordinates, grad_output, grad_laplacian, batch, whole, seed,
                                        tile + slots, w, m);
       }
       const float x0 = in.x0, x1 = in.x1;
@@ -1440,13 +1683,57 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         }
       }
     }
+    // kRest: interior points past the last whole round of 64-point tiles, as 16-point tiles
+    // whose rows are split over the 4 waves (split_tile), so a round that is not whole costs a
+    // quarter tile on the slots that have one instead of a whole tile on some. The scratch
+    // overlays the dW staging buffer: the barrier waits for the last 64-point tile's readers.
+    // (A separate instantiation: with this loop in the kernel the compiler schedules the
+    // 64-point loop differently, about 0.5 % slower, so whole rounds run without it.)
+    if (kRest && tile < interior_end) {  // uniform per workgroup
+      __syncthreads();
+      const SplitScratch scratch{
+          s_stage, reinterpret_cast<f4 (*)[kSplitWaves][4][kWave]>(s_stage + 3 * kTPlane),
+          reinterpret_cast<float (*)[kTWave]>(s_stage + 3 * kTPlane + 2 * kSplitWaves * 4 * kWave * 4),
+          reinterpret_cast<float (*)[2][kTile]>(s_stage + 3 * kTPlane +
+                                                2 * kSplitWaves * 4 * kWave * 4 +
+                                                kSplitWaves * kTWave)};
+      int phase = 0;
+      for (; tile < interior_end; tile += slots) {
+        keep_lds_reads_in_loop();
+        const int m_pick = opaque(m);
+        const TileInputs in = next;
+        if (tile + slots < tiles) {
+          next = load_tile_inputs<kLoss, kRest>(coordinates, grad_output, grad_laplacian, batch, whole,
+                                         seed, tile + slots, w, m);
+        }
+        const int64_t point = whole * kBwdTile + (tile - whole) * kTile + m;
+        SplitSums sums{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        split_tile<kLoss>(s_w, s_small, scratch, phase, w, g, m_pick,
+                          opaque(rows_off) + 1088 * w, opaque(cols_off) + 16 * w,
+                          m_pick * kWRow + 4 * g, in.x0, in.x1, kLoss ? 0.f : in.a,
+                          kLoss ? 0.f : in.b, kLoss ? in.a : 0.f, point < batch, false, point,
+                          grad_coordinates, seed, acc.dw, acc.bh, sums);
+        // Into this wave's owned-neuron lanes (owned_neuron): the wave's rows only; the point
+        // sums shared by the 4 waves from wave 0 alone.
+        const bool own = (m_pick >> 2) == w;
+        acc.w0x += own ? sums.w0x : 0.f;
+        acc.w0y += own ? sums.w0y : 0.f;
+        acc.b0 += own ? sums.b0 : 0.f;
+        acc.wout += own ? sums.wout : 0.f;
+        if (w == 0) {
+          acc.bout += sums.bout;
+          acc.loss += sums.loss;
+        }
+        deliver(next);
+      }
+    }
     if (kLoss) {
       for (; tile < tiles; tile += slots) {  // boundary tiles (uniform per workgroup)
         keep_lds_reads_in_loop();
         const int m_pick = opaque(m);
         const TileInputs in = next;
         if (tile + slots < tiles) {
-          next = load_tile_inputs<kLoss>(coordinates, grad_output, grad_laplacian, batch, seed,
+          next = load_tile_inputs<kLoss, kRest>(coordinates, grad_output, grad_laplacian, batch, whole, seed,
                                          tile + slots, w, m);
         }
         const int64_t point = (tile - seed.interior_tiles) * kTile + m;
@@ -1518,22 +1805,6 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 // choice between the two kernels depends only on the batch, so results do not depend on the
 // device. The tanh-jet, adjoint and loss arithmetic is backward_kernel's; the sums over points
 // are grouped differently, so the two kernels agree to rounding, not bitwise.
-constexpr int kSplitBwdMaxTiles = 768;  // backward_split_kernel up to 768 16-point tiles
-constexpr int kTPlane = 64 * kWRow;     // floats of one transposed 64-row layer (h)
-constexpr int kTWave = 16 * kWRow;      // floats of one wave's transposed zbar
-
-// Store this lane's 4 rows (rows0 + 4 g + r) x 4 components at point m into a transposed
-// buffer t[row][68]: component c of point p = 4 s + g' at t[row * 68 + 16 c + 4 g' + s].
-__device__ __forceinline__ void store_transposed(float* t, int rows0, int g, int m,
-                                                 const f4 (&x)[4]) {
-  const int col = 4 * (m & 3) + (m >> 2);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) t[(rows0 + 4 * g + r) * kWRow + 16 * c + col] = x[c][r];
-  }
-}
-
 template <bool kLoss>
 __global__ void __launch_bounds__(kSplitWaves * kWave, 1)
 backward_split_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
@@ -1559,6 +1830,7 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
   const int cols_off = lane_cols(m, g) + 16 * w;    // W[.][16 w + m] (transposed operand)
   const int t_read = m * kWRow + 4 * g;             // transposed reads: row m, points 4 s + g
 
+  const SplitScratch scratch{s_ht, s_x, s_zt, s_gx};
   int phase = 0;  // alternates the s_x buffers
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
     f4 dw[3][4];
@@ -1591,188 +1863,17 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
         }
       }
 
-      // ---- forward re-run: all 64 rows of layer 0, then this wave's rows of layers 1..3 ----
-      f4 h[4][4];
-      layer0_forward(s_small, g, x0, x1, h);
-      {
-        f4 own[4];  // this wave's block again (h[w] would need a dynamic register index)
-        layer0_block(s_small, w, g, x0, x1, own);
-        store_transposed(s_ht, 16 * w, g, m, own);
-      }
-      f4 z[3][4];  // this wave's pre-activations of hidden layers 1..3
-      f4 mine[4];  // this wave's rows of the current layer output
-#pragma unroll
-      for (int layer = 0; layer < 3; ++layer) {
-        const f4 b = lds4(s_small + kSmallBh + layer * kHidden + 16 * w + 4 * g);
-        const float* wrow = s_w + layer * kPlane + opaque(rows_off);
-#pragma unroll
-        for (int ob = 0; ob < 4; ++ob) {
-          const f4 a = lds4(wrow + 16 * ob);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const f4 cin = (ob | j) ? z[layer][c] : (c == 0 ? b : zero4());
-              z[layer][c] = mfma(a[j], h[ob][c][j], cin);
-            }
-          }
-        }
-        tanh_jet4(z[layer], mine);
-        f4 (*xb)[4][kWave] = s_x[phase];
-        phase ^= 1;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) xb[w][c][lane] = mine[c];
-        if (layer < 2) store_transposed(s_ht + (layer + 1) * kTPlane, 16 * w, g, m, mine);
-        __syncthreads();
-#pragma unroll
-        for (int ob = 0; ob < 4; ++ob) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) h[ob][c] = xb[ob][c][lane];  // this wave's block included
-        }
-      }
-
-      if (kLoss) {
-        // u (boundary) or lap (interior) over all 64 rows, in backward_kernel's order.
-        float out = 0.0f;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const f4 wo = lds4(s_small + (on_boundary ? kSmallWoutV : kSmallWoutL) + 16 * mb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            out = __builtin_fmaf(wo[r], on_boundary ? h[mb][0][r] : h[mb][3][r], out);
-          }
-        }
-        out = sum_lane_groups(out);
-        if (on_boundary) {
-          const float u = active ? out + s_small[kSmallBout] : 0.0f;
-          gu = seed.boundary_scale * (2.0f * u);
-          g_bloss += sum_row16(u * u);
-        } else {
-          const float res = active ? out - f : 0.0f;
-          gl = seed.inv_batch * (2.0f * res);
-          g_loss += sum_row16(res * res);
-        }
-      }
-
-      // ---- output layer: this wave's rows of the seed and of dw_out ----
-      f4 hb[4];
-      {
-        const float gu_c = gu * (4.0f / kC);
-        const float gl_l = gl * (4.0f / kLambda);
-        const f4 wv = lds4(s_small + kSmallWoutV + 16 * w + 4 * g);
-        const f4 wl = lds4(s_small + kSmallWoutL + 16 * w + 4 * g);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float total = sum_row16(__builtin_fmaf(gu_c, mine[0][r], gl_l * mine[3][r]));
-          g_wout = (m & 3) == r ? g_wout + total : g_wout;
-          hb[0][r] = gu * wv[r];
-          hb[1][r] = 0.0f;
-          hb[2][r] = 0.0f;
-          hb[3][r] = gl * wl[r];
-        }
-        g_bout += sum_row16(gu);
-      }
-
-      // ---- hidden layers 3, 2, 1 ----
-#pragma unroll
-      for (int layer = 2; layer >= 0; --layer) {
-        // zbar of this wave's rows (tanh-jet adjoint, lane-local)
-        f4 zb[4];
-        f4 v4, s4;
-        tanh_scaled4(z[layer][0], v4, s4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float v = v4[r], s = s4[r];
-          float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
-          tanh_jet_adjoint_vs(v, s, z[layer][1][r], z[layer][2][r], z[layer][3][r], bv, bj0, bj1,
-                              bl);
-          zb[0][r] = bv;
-          zb[1][r] = bj0;
-          zb[2][r] = bj1;
-          zb[3][r] = bl;
-        }
-        f4 (*xb)[4][kWave] = s_x[phase];
-        phase ^= 1;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) xb[w][c][lane] = zb[c];
-        float* zt = &s_zt[w][0];
-        store_transposed(zt, 0, g, m, zb);
-        __syncthreads();
-        // dW[16 w + ., 16 nb + .] += sum over (c, points) of zbar h_prev^T; the A reads of
-        // component 0 also give the bias sum of row 16 w + m.
-        {
-          const float* ht = s_ht + layer * kTPlane + opaque(t_read);
-          const float* za = zt + opaque(t_read);
-          float bsum = 0.0f;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            const f4 a = lds4(za + 16 * c);
-            f4 bt[4];
-#pragma unroll
-            for (int nb = 0; nb < 4; ++nb) bt[nb] = lds4(ht + 16 * kWRow * nb + 16 * c);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              if (c == 0) bsum += a[s];
-#pragma unroll
-              for (int nb = 0; nb < 4; ++nb) dw[layer][nb] = mfma(a[s], bt[nb][s], dw[layer][nb]);
-            }
-          }
-          bias[layer] += sum_lane_groups(bsum);
-        }
-        // hbar of this wave's rows of the layer below: sum over all 64 rows o of
-        // W[o][16 w + .] zbar[o].
-        {
-          const float* wt = s_w + layer * kPlane + opaque(cols_off);
-#pragma unroll
-          for (int ob = 0; ob < 4; ++ob) {
-            f4 zo[4];  // zbar of rows 16 ob .. 16 ob + 15 (this wave's block included)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) zo[c] = xb[ob][c][lane];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const float a = wt[1088 * ob + kWRow * j];
-#pragma unroll
-              for (int c = 0; c < 4; ++c) hb[c] = mfma(a, zo[c][j], (ob | j) ? hb[c] : zero4());
-            }
-          }
-        }
-      }
-
-      // ---- layer 0 for this wave's rows: dW0, db0 and this wave's part of grad_x ----
-      {
-        const Layer0Weights w0 = layer0_weights(s_small, w, g);
-        const float cx0 = kHalfC * x0, cx1 = kHalfC * x1;
-        float gx0 = 0.f, gx1 = 0.f;
-        f4 zv4, v4, s4;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) zv4[r] = layer0_zv(w0, r, x0, x1);
-        tanh_scaled4(zv4, v4, s4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float v = v4[r], s = s4[r];
-          float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
-          tanh_jet_adjoint_vs(v, s, w0.wx[r], w0.wy[r], 0.0f, bv, bj0, bj1, bl);
-          gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
-          gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
-          const float t0 = sum_row16(__builtin_fmaf(bv, cx0, bj0));
-          const float t1 = sum_row16(__builtin_fmaf(bv, cx1, bj1));
-          const float tb = sum_row16(bv);
-          g_w0x = (m & 3) == r ? g_w0x + t0 : g_w0x;
-          g_w0y = (m & 3) == r ? g_w0y + t1 : g_w0y;
-          g_b0 = (m & 3) == r ? g_b0 + tb : g_b0;
-        }
-        gx0 = sum_lane_groups(gx0);
-        gx1 = sum_lane_groups(gx1);
-        if (g == 0) {
-          s_gx[w][0][m] = gx0;
-          s_gx[w][1][m] = gx1;
-        }
-        __syncthreads();
-        if (w == 0 && g == 0 && active && (!kLoss || (grad_coordinates != nullptr && !on_boundary))) {
-          grad_coordinates[2 * point] = ((s_gx[0][0][m] + s_gx[1][0][m]) + s_gx[2][0][m]) + s_gx[3][0][m];
-          grad_coordinates[2 * point + 1] = ((s_gx[0][1][m] + s_gx[1][1][m]) + s_gx[2][1][m]) + s_gx[3][1][m];
-        }
-      }
+      SplitSums sums{g_w0x, g_w0y, g_b0, g_wout, g_bout, g_loss, g_bloss};
+      split_tile<kLoss>(s_w, s_small, scratch, phase, w, g, m, rows_off, cols_off, t_read, x0, x1,
+                        gu, gl, f, active, on_boundary, point, grad_coordinates, seed, dw, bias,
+                        sums);
+      g_w0x = sums.w0x;
+      g_w0y = sums.w0y;
+      g_b0 = sums.b0;
+      g_wout = sums.wout;
+      g_bout = sums.bout;
+      g_loss = sums.loss;
+      g_bloss = sums.bloss;
     }
 
     // ---- this slot's partial row: each wave writes its own rows ----
@@ -1997,6 +2098,22 @@ size_t workspace_bytes_for(int slots) {
 
 int64_t split_tiles(int64_t points) { return (points + kTile - 1) / kTile; }
 
+// Interior tiles of backward_kernel for `batch` points over `slots` slots: 64-point tiles in
+// whole rounds of `slots` (`whole` of them), then the remaining points as 16-point tiles whose
+// rows are split over the waves (`total` counts both). Below one whole round, or when the
+// rounds are whole, every tile is a 64-point one.
+struct InteriorTiles {
+  int64_t whole, total;
+};
+
+InteriorTiles interior_tiles_for(int64_t batch, int slots) {
+  const int64_t t64 = backward_tiles(batch);
+  const int64_t rounds = t64 / slots;
+  if (rounds == 0 || t64 % slots == 0) return {t64, t64};
+  const int64_t whole = rounds * slots;
+  return {whole, whole + split_tiles(batch - whole * kBwdTile)};
+}
+
 // Gradient kernel for `batch` interior and `boundary_count` boundary points:
 // backward_split_kernel up to kSplitBwdMaxTiles 16-point tiles, chosen from the batch alone
 // so that results do not depend on the device. FUSED_HOAD_BWD_SPLIT=0 / 1 (experiment knob,
@@ -2140,10 +2257,19 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
   } else {
     slots = backward_slots(batch);
     if (int st = backward_grid(slots, &grid)) return st;
+    const InteriorTiles it = interior_tiles_for(batch, slots);
     f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
-    hipLaunchKernelGGL(backward_kernel<false>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
-                       coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
-                       partials, stash, batch, backward_tiles(batch), slots, LossSeed{});
+    if (it.whole != it.total) {
+      hipLaunchKernelGGL((backward_kernel<false, true>), dim3(grid), dim3(kBwdWaves * kWave), 0,
+                         hs, coordinates, parameters, grad_output, grad_laplacian,
+                         grad_coordinates, partials, stash, batch, it.whole, it.total, slots,
+                         LossSeed{});
+    } else {
+      hipLaunchKernelGGL((backward_kernel<false, false>), dim3(grid), dim3(kBwdWaves * kWave), 0,
+                         hs, coordinates, parameters, grad_output, grad_laplacian,
+                         grad_coordinates, partials, stash, batch, it.whole, it.total, slots,
+                         LossSeed{});
+    }
     if (int st = check_launch("backward_kernel")) return st;
   }
   hipLaunchKernelGGL(reduce_partials_kernel, dim3((kParameterCount + 63) / 64),
@@ -2179,9 +2305,12 @@ extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* so
   }
   if (int st = check_workspace_alignment(workspace)) return st;
   const bool split = use_split_backward(batch, boundary_count);
-  const int64_t interior_tiles = split ? split_tiles(batch) : backward_tiles(batch);
+  const int slots = slots_for_tiles((split ? split_tiles(batch) : backward_tiles(batch)) +
+                                    split_tiles(boundary_count));
+  const InteriorTiles it =
+      split ? InteriorTiles{0, split_tiles(batch)} : interior_tiles_for(batch, slots);
+  const int64_t interior_tiles = it.total;
   const int64_t tiles = interior_tiles + split_tiles(boundary_count);  // 16-point boundary tiles
-  const int slots = slots_for_tiles(tiles);
   int grid = 0;
   if (int st = backward_grid(slots, &grid)) return st;
   const hipStream_t hs = static_cast<hipStream_t>(stream);
@@ -2198,9 +2327,15 @@ extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* so
     if (int st = check_launch("backward_split_kernel")) return st;
   } else {
     f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
-    hipLaunchKernelGGL(backward_kernel<true>, dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
-                       coordinates, parameters, nullptr, nullptr, grad_coordinates, partials,
-                       stash, batch, tiles, slots, seed);
+    if (it.whole != it.total) {
+      hipLaunchKernelGGL((backward_kernel<true, true>), dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
+                         coordinates, parameters, nullptr, nullptr, grad_coordinates, partials,
+                         stash, batch, it.whole, tiles, slots, seed);
+    } else {
+      hipLaunchKernelGGL((backward_kernel<true, false>), dim3(grid), dim3(kBwdWaves * kWave), 0,
+                         hs, coordinates, parameters, nullptr, nullptr, grad_coordinates,
+                         partials, stash, batch, it.whole, tiles, slots, seed);
+    }
     if (int st = check_launch("backward_kernel")) return st;
   }
   const AdamArgs args{parameters, exp_avg, exp_avg_sq, step, loss, grad_parameters,

@@ -139,6 +139,25 @@ def test_backward_is_bitwise_deterministic_across_runs_grids_and_versions() -> N
             os.environ["FUSED_HOAD_BWD_BLOCKS"] = saved
 
 
+def test_backward_past_the_last_whole_round() -> None:
+    """70,001 points are 4 whole rounds of 64-point tiles on 256 slots plus 4,465 points, which
+    run as 16-point tiles shared by the workgroup's 4 waves: against the recompute backward,
+    and bitwise the same for every grid."""
+    announce("backward past the last whole round, batch=70001, FUSED_HOAD_BWD_BLOCKS in {1, 7, 256}")
+    p = packed(0)
+    x = coordinates(70001, seed=11)
+    gu, gl = upstream(70001, seed=11)
+    ref_p, ref_x = _fused_backward(x, p, gu, gl)
+    ep, ex = torch_ref.recompute_backward(p, x, gu, gl)
+    for name, lo, hi in BLOCKS:
+        assert_scaled_close(ref_p[lo:hi], ep[lo:hi], 1e-4, name)
+    assert_scaled_close(ref_x, ex, 1e-4, "grad_coordinates")
+    for blocks in ("1", "7", "256"):
+        with knobs(FUSED_HOAD_BWD_BLOCKS=blocks):
+            gp, gx = _fused_backward(x, p, gu, gl)
+        assert torch.equal(gp, ref_p) and torch.equal(gx, ref_x), f"changed with {blocks} blocks"
+
+
 @pytest.mark.parametrize("batch", [1, 17, 1000, 4096, 12288])
 def test_split_backward_agrees_with_the_tiled_kernel(batch: int) -> None:
     """Up to 768 16-point tiles the backward runs backward_split_kernel (rows split over a
