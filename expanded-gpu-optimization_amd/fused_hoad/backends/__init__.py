@@ -1,8 +1,10 @@
 """Interchangeable implementations of ``model -> (u, Laplacian(u))``.
 
 Every backend takes a dense MLP and ``[batch, dims]`` coordinates and returns the output and
-its input Laplacian, both ``[batch, 1]``. ``eager`` is the registry's oracle. The ``fused_*``
-entries run the gfx950 kernels; they are registered only when the extension is built.
+its input Laplacian, both ``[batch, 1]``. ``eager`` is the registry's oracle. The ``*_cudagraph``
+entries replay a HIP graph of their base backend (inference only; the base backend off the
+GPU). The ``fused_*`` entries run the gfx950 kernels; they are registered only when the
+extension is built.
 Registry keys follow /root/reference/src/fused_hoad/backends/__init__.py:22-67; every
 ``fused_cuda*`` name maps onto the one forward kernel and the one backward kernel pair.
 """
@@ -15,15 +17,20 @@ from torch import Tensor, nn
 from fused_hoad._extension import extension_available
 from fused_hoad.backends.eager import eager_laplacian
 from fused_hoad.backends.forward_laplacian import forward_laplacian
+from fused_hoad.backends.func import func_laplacian
+from fused_hoad.backends.graphs import cuda_graphed
 
 Backend = Callable[[nn.Module, Tensor], tuple[Tensor, Tensor]]
 
 BACKENDS: dict[str, Backend] = {
     "eager": eager_laplacian,
+    "eager_cudagraph": cuda_graphed(eager_laplacian),
+    "func": func_laplacian,
     "forward_laplacian": forward_laplacian,
+    "forward_laplacian_cudagraph": cuda_graphed(forward_laplacian),
 }
 
-TRAINABLE_BACKENDS = ("eager", "forward_laplacian")
+TRAINABLE_BACKENDS = ("eager", "func", "forward_laplacian")
 
 FIXED_CONTRACT_BACKENDS: tuple[str, ...] = ()
 if extension_available():
@@ -63,7 +70,9 @@ __all__ = [
     "REFERENCE_BACKEND",
     "TRAINABLE_BACKENDS",
     "Backend",
+    "cuda_graphed",
     "eager_laplacian",
     "forward_laplacian",
+    "func_laplacian",
     "get_backend",
 ]

@@ -108,6 +108,27 @@ def test_forward_laplacian_matches_eager_in_float64(config) -> None:
     torch.testing.assert_close(lap, el, atol=1e-10, rtol=1e-8)
 
 
+@pytest.mark.parametrize("config", CONFIGS, ids=lambda c: f"{c.activation}-{c.input_dim}d")
+def test_func_backend_matches_eager_in_float64(config) -> None:
+    model, x = _model_and_coordinates(config)
+    eu, el = get_backend("eager")(model, x)
+    u, lap = get_backend("func")(model, x)
+    assert u.shape == lap.shape == (x.shape[0], 1)
+    torch.testing.assert_close(u, eu, atol=1e-12, rtol=1e-10)
+    torch.testing.assert_close(lap, el, atol=1e-10, rtol=1e-8)
+    with pytest.raises(ValueError, match="batch, dimensions"):
+        get_backend("func")(model, x[0])
+
+
+@pytest.mark.parametrize("name", ["eager", "forward_laplacian"])
+def test_graph_backends_call_their_base_backend_off_the_gpu(name: str) -> None:
+    model, x = _model_and_coordinates(DEFAULT_POISSON_MLP, batch=16)
+    want = get_backend(name)(model, x)
+    got = get_backend(f"{name}_cudagraph")(model, x)
+    for g, w in zip(got, want, strict=True):
+        assert torch.equal(g, w)
+
+
 def test_forward_laplacian_matches_oracle_jet() -> None:
     model, x = _model_and_coordinates(DEFAULT_POISSON_MLP, batch=40)
     flat = pack_poisson_parameters(model)
