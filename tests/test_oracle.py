@@ -191,3 +191,95 @@ def test_pack_unpack_round_trip_and_offsets() -> None:
     assert params.b[0][0] == 4288 and params.w[1][0, 0] == 4352 and params.b[2][63] == 12671
     assert params.w_out[0] == 12672 and params.b_out == 12736
     np.testing.assert_array_equal(jet.pack(params), flat)
+
+
+# ---- the CPU training-step baseline: poisson_source and eager_train_step ----
+
+
+def test_poisson_source_is_the_laplacian_of_the_manufactured_solution() -> None:
+    """f = -2 pi^2 sin(pi x) sin(pi y) is pinned by known values and by a float64 five-point
+    finite-difference Laplacian of u* = sin(pi x) sin(pi y) (truncation error
+    h^2 / 12 * 2 pi^4 |u*| < 2e-5 at h = 1e-3), which a wrong sign or factor fails."""
+    pi2 = np.pi**2
+    known = torch.tensor([[0.5, 0.5], [-0.5, 0.5], [0.5, -0.5], [0.0, 0.3], [0.7, 1.0], [-1.0, -1.0]],
+                         dtype=torch.float64)
+    np.testing.assert_allclose(torch_ref.poisson_source(known).numpy().ravel(),
+                               [-2 * pi2, 2 * pi2, 2 * pi2, 0.0, 0.0, 0.0], rtol=1e-15, atol=1e-13)
+
+    def solution(p):
+        return np.sin(np.pi * p[:, 0]) * np.sin(np.pi * p[:, 1])
+
+    def laplacian_fd(p, h=1e-3):
+        total = -4.0 * solution(p)
+        for d in range(2):
+            step = np.zeros_like(p)
+            step[:, d] = h
+            total += solution(p + step) + solution(p - step)
+        return total / h**2
+
+    x = _coords(200, 21)
+    got = torch_ref.poisson_source(torch.tensor(x)).numpy().ravel()
+    assert torch_ref.poisson_source(torch.tensor(x)).shape == (200, 1)
+    np.testing.assert_allclose(got, laplacian_fd(x), rtol=0, atol=5e-5)
+    # planted mistakes (sign, pi instead of pi^2) fail the same check
+    assert not np.allclose(-got, laplacian_fd(x), rtol=0, atol=5e-5)
+    assert not np.allclose(got / np.pi, laplacian_fd(x), rtol=0, atol=5e-5)
+
+
+def _eager_step_matches_the_oracle(step_fn=None) -> bool:
+    """One eager_train_step in float64 (Adam lr 1e-3 from zero state) against
+    oracle/adam.poisson_adam_step: the loss, the 12,737 gradients and the updated parameters.
+    Returns False on a mismatch or when the step cannot run."""
+    from oracle import adam
+
+    model = torch_ref.reference_model(0).double()
+    x = torch.tensor(_coords(256, 22))
+    source = torch_ref.poisson_source(x)
+    p0 = torch_ref.pack(model).numpy().copy()
+    optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)
+    try:
+        loss = (step_fn or torch_ref.eager_train_step)(model, x, source, optimizer)
+    except RuntimeError:
+        return False
+    # b_out does not reach the Laplacian, so autograd leaves its .grad unset (the oracle: 0)
+    grads = torch.cat([(t.grad if t.grad is not None else torch.zeros_like(t)).reshape(-1)
+                       for m in model if isinstance(m, torch.nn.Linear) for t in (m.weight, m.bias)]).numpy()
+    want = adam.poisson_adam_step(p0, x.numpy(), source.numpy().ravel(), np.zeros_like(p0),
+                                  np.zeros_like(p0), 1)
+    return bool(
+        abs(float(loss) - want["loss"]) <= 1e-12 * abs(want["loss"])
+        and np.allclose(grads, want["grad_parameters"], rtol=0, atol=1e-11 * np.abs(want["grad_parameters"]).max())
+        and np.allclose(torch_ref.pack(model).numpy(), want["params"], rtol=0, atol=1e-13)
+    )
+
+
+def test_eager_train_step_matches_the_float64_oracle_step() -> None:
+    assert _eager_step_matches_the_oracle()
+
+
+def test_eager_train_step_planted_mistakes_are_caught(monkeypatch: pytest.MonkeyPatch) -> None:
+    """Two mistakes planted in the step's nested autograd: dropping create_graph from the
+    second-derivative passes (the loss no longer reaches the weights) and dropping the y
+    second derivative from the Laplacian. The oracle-step check must reject both."""
+    real_grad = torch.autograd.grad
+
+    def planted(mistake):
+        calls = []
+
+        def grad(outputs, inputs, *args, **kwargs):
+            calls.append(None)
+            nested = len(calls) > 1  # calls 2 and 3 are the second derivatives (d = 0, 1)
+            if mistake == "create_graph" and nested:
+                kwargs["create_graph"] = False
+            result = real_grad(outputs, inputs, *args, **kwargs)
+            if mistake == "y_term" and len(calls) == 3:
+                result = tuple(r * 0.0 for r in result)
+            return result
+
+        return grad
+
+    for mistake in ("create_graph", "y_term"):
+        monkeypatch.setattr(torch.autograd, "grad", planted(mistake))
+        assert not _eager_step_matches_the_oracle(), mistake
+        monkeypatch.setattr(torch.autograd, "grad", real_grad)
+    assert _eager_step_matches_the_oracle()
