@@ -4,11 +4,17 @@ Metric: residual points/s (u, Laplacian u) at 64K points plus tr
 64K points, FP32, 1 GPU. One "step" is one fused residual evaluation of 65,536 points
 (coordinates already in HBM). The training step (forward jet, loss mean((Laplacian u - f)^2)
 with f = -2 pi^2 sin(pi x) sin(pi y), adjoint jet, Adam lr 1e-3) is timed the same way at 65,536
-points: ``train_step_ms`` is the fused step (FusedPoissonAdam: one gradient kernel that re-runs
-the forward and seeds itself from the loss, one reduction kernel with the Adam update),
-``train_step_graphed_ms`` the same replayed from a HIP graph, and ``train_step_autograd_ms``
-the reference's step through the drop-in API (fused forward + autograd loss + fused backward +
-torch.optim.Adam).
+points with all of BASELINE config 3's outputs (gradients of every weight and bias and of the
+input coordinates): ``train_step_ms`` is the fused step (FusedPoissonAdam: one gradient kernel
+that re-runs the forward and seeds itself from the loss, one reduction kernel with the Adam
+update), ``train_step_graphed_ms`` the same replayed from a HIP graph, and
+``train_step_autograd_ms`` the reference's step through the drop-in API (fused forward +
+autograd loss + fused backward + torch.optim.Adam). ``train_step_no_coordinate_grad_ms`` is
+the fused step without the coordinate gradient, a labelled variant only.
+
+``roofline.traffic`` comes from the committed rocprofv3 summary
+profiles/forward_kernel_65536_traffic.json only when that was measured on the kernel source
+this run executes (same SHA-256); otherwise it is null and ``traffic_source`` says why.
 
 Timing: the residual first runs untimed for --settle-seconds (0.3 s by default), because the
 shader clock needs about 0.1 s of sustained load to reach its steady level and a few warmup
@@ -29,6 +35,7 @@ Prints human-readable lines to stderr and ONE JSON line to stdout.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import statistics
@@ -46,6 +53,7 @@ FLOP_PER_POINT_BACKWARD = 2 * FLOP_PER_POINT_FORWARD  # dW + hbar (recompute not
 REFERENCE_A5000 = {"residual_points_per_s_64k": 121.9e6, "train_step_ms_64k": 3.334,
                    "hardware": "RTX A5000", "source": "reference results/2026-11-06-RTX-A5000-8454035"}
 TRAFFIC_FILE = ROOT / "profiles" / "forward_kernel_65536_traffic.json"
+KERNEL_SOURCE = ROOT / "expanded-gpu-optimization_amd" / "csrc" / "fused_hoad_kernels.hip"
 CPU_RESIDUAL_CALLS = 200     # CPU baseline sample sizes (see _cpu_baseline)
 CPU_RESIDUAL_1K_CALLS = 200
 CPU_STEP_CALLS = 40
@@ -132,6 +140,29 @@ def _per_call_events(fn, iterations: int, torch) -> list[float]:
 def _p90(samples: list[float]) -> float:
     ordered = sorted(samples)
     return ordered[min(len(ordered) - 1, int(0.9 * len(ordered)))]
+
+
+def _kernel_source_sha256() -> str:
+    return hashlib.sha256(KERNEL_SOURCE.read_bytes()).hexdigest()
+
+
+def _measured_traffic(points: int):
+    """HBM bytes per forward launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary, used only when it was measured on this workload AND on the kernel source this
+    run executes (its SHA-256 is recorded in the file); otherwise None, with the reason."""
+    if not TRAFFIC_FILE.exists():
+        return None, "no committed measurement"
+    measured = json.loads(TRAFFIC_FILE.read_text())
+    where = str(TRAFFIC_FILE.relative_to(ROOT))
+    if measured.get("points") != points:
+        return None, f"{where} holds {measured.get('points')} points, not {points}"
+    current = _kernel_source_sha256()
+    if measured.get("kernel_source_sha256") != current:
+        return None, (f"stale: {where} was measured on kernel source "
+                      f"{str(measured.get('kernel_source_sha256'))[:12]}, this run's is {current[:12]}")
+    return measured.get("hbm_bytes_per_launch"), {
+        "file": where, "kernel_source_sha256": current, "commands": measured.get("commands"),
+    }
 
 
 def _scaled_error(actual, expected) -> float:
@@ -238,23 +269,28 @@ def main() -> None:
     log(f"train step (autograd drop-in) {args.train_points} pts: {autograd_ms:.3f} ms wall/step")
 
     # ---- training step (b): the fused step, FusedPoissonAdam (2 kernels) ----
+    # All of config 3's outputs: the gradients of every weight and bias and of the input
+    # coordinates (they require grad, so each step writes trainer.grad_coordinates, as the
+    # reference's backward always writes grad_coordinates, csrc/fused_backward.cu:830-831).
     torch.manual_seed(0)
     fused_model = build_mlp(DEFAULT_POISSON_MLP).to(device)
-    trainer = FusedPoissonAdam(fused_model, x_train, source, lr=1e-3)
-    # check the first step before timing: loss against the fused forward's, gradient against
-    # the recompute backward seeded with grad_lap = 2 (lap - f) / B
+    x_train_grad = x_train.detach().clone().requires_grad_(True)
+    trainer = FusedPoissonAdam(fused_model, x_train_grad, source, lr=1e-3)
+    # check the first step before timing: loss against the fused forward's, parameter and
+    # coordinate gradients against the recompute backward seeded with grad_lap = 2 (lap - f) / B
     with torch.no_grad():
         _, lap0 = fused_forward_laplacian(x_train, trainer.parameters)
     resid0 = lap0 - source
     want_loss = resid0.double().pow(2).mean().item()
-    _, want_grad = _recompute_backward(x_train, trainer.parameters.clone(), torch.zeros_like(lap0),
-                                       2.0 * resid0 / args.train_points, False, True)
+    want_grad_x, want_grad = _recompute_backward(x_train, trainer.parameters.clone(), torch.zeros_like(lap0),
+                                                 2.0 * resid0 / args.train_points, True, True)
     got_loss = trainer.step().item()
-    step_err = _scaled_error(trainer.grad, want_grad)
+    step_err = max(_scaled_error(trainer.grad, want_grad),
+                   _scaled_error(trainer.grad_coordinates, want_grad_x))
     if abs(got_loss - want_loss) > 1e-5 * abs(want_loss) or step_err > 1e-4:
         raise SystemExit(f"fused step disagrees: loss {got_loss} vs {want_loss}, gradient {step_err:.3e}")
     log(f"check: fused step loss rel error {abs(got_loss - want_loss) / want_loss:.2e}, "
-        f"gradient max scaled error {step_err:.2e}")
+        f"parameter and coordinate gradients max scaled error {step_err:.2e}")
     for _ in range(args.warmup):
         trainer.step()
     torch.cuda.synchronize()
@@ -264,9 +300,20 @@ def main() -> None:
     train_ms = train_total_ms / args.steps
     peak_mib = (torch.cuda.max_memory_allocated(device) - baseline_bytes) / 2**20
     train_calls = _per_call_events(trainer.step, args.steps, torch)
-    log(f"train step (fused) {args.train_points} pts: {train_ms:.3f} ms wall/step, "
+    log(f"train step (fused, with coordinate gradients) {args.train_points} pts: {train_ms:.3f} ms wall/step, "
         f"{train_gpu_ms / args.steps:.3f} ms GPU/step; per-call events median {statistics.median(train_calls):.3f} ms, "
         f"p90 {_p90(train_calls):.3f} ms; backward call {bwd_ms * 1e3:.1f} us; peak {peak_mib:.1f} MiB above baseline")
+
+    # labelled variant: the same step on coordinates that do not require grad (no
+    # grad_coordinates store), for comparison with earlier records only
+    torch.manual_seed(0)
+    plain_trainer = FusedPoissonAdam(build_mlp(DEFAULT_POISSON_MLP).to(device), x_train, source, lr=1e-3)
+    for _ in range(args.warmup + 1):
+        plain_trainer.step()
+    plain_total_ms, _ = _timed(plain_trainer.step, args.steps, torch)
+    plain_ms = plain_total_ms / args.steps
+    log(f"train step (fused, no coordinate gradients) {args.train_points} pts: {plain_ms:.3f} ms wall/step")
+    del plain_trainer
 
     # ---- training step (c): the fused step replayed from a HIP graph ----
     replay = trainer.graphed(warmup=1)
@@ -288,11 +335,7 @@ def main() -> None:
     clock = _gpu_clock_mhz()
     fwd_tflops = FLOP_PER_POINT_FORWARD * args.points / (fwd_kernel_ms / 1e3) / 1e12
     bwd_tflops = FLOP_PER_POINT_BACKWARD * args.train_points / (bwd_ms / 1e3) / 1e12
-    traffic = None  # measured HBM bytes per launch, known only for the profiled workload
-    if TRAFFIC_FILE.exists():
-        measured = json.loads(TRAFFIC_FILE.read_text())
-        if measured.get("points") == args.points:
-            traffic = measured.get("hbm_bytes_per_launch")
+    traffic, traffic_source = _measured_traffic(args.points)
     roofline = {
         "bound": "mfma",
         "achieved": round(fwd_tflops, 3),
@@ -300,6 +343,7 @@ def main() -> None:
         "unit": "TFLOP/s",
         "frac": round(fwd_tflops / PEAK_FP32_MATRIX_TFLOPS, 4),
         "traffic": traffic,
+        "traffic_source": traffic_source,
         "kernel": "forward_kernel",
         "flop_per_launch": FLOP_PER_POINT_FORWARD * args.points,
         "avg_launch_ms": round(fwd_kernel_ms, 5),
@@ -354,6 +398,8 @@ def main() -> None:
             "train_points": args.train_points,
         },
         "train_step_ms": round(train_ms, 5),
+        "train_step_outputs": "loss, gradients of all 12,737 parameters and of the 65,536 x 2 input coordinates, Adam update",
+        "train_step_no_coordinate_grad_ms": round(plain_ms, 5),
         "train_step_tflops": round(train_tflops, 3),
         "train_step_peak_mib": round(peak_mib, 2),
         "train_step_graphed_ms": round(graph_ms, 5),

@@ -40,8 +40,12 @@ def _blocks():
         yield f"{spec.name}.bias", spec.bias_offset, spec.end_offset
 
 
-@pytest.mark.parametrize("batch", [1, 63, 1000, 4096, 20000])
+@pytest.mark.parametrize("batch", [1, 63, 1000, 4096, 20000, 65536])
 def test_one_step_matches_the_oracle(batch: int) -> None:
+    """Loss, all 10 gradient blocks, the coordinate gradient and the Adam update of one step
+    against the float64 oracle. 65,536 is BASELINE config 3 (whole rounds of 64-point tiles on
+    every slot, coordinates requiring grad), the reference's per-block backward check at that
+    size being /root/reference/tests/test_fused.py:194-218."""
     announce(f"fused Poisson+Adam step vs float64 oracle, batch={batch}")
     from oracle import adam
     from fused_hoad.training import FusedPoissonAdam
