@@ -2091,10 +2091,20 @@ int backward_slots(int64_t batch) { return slots_for_tiles(backward_tiles(batch)
 
 // Workspace of the gradient kernel for `slots` slots: the partial rows, then one z stash per
 // (workgroup, wave); the grid never exceeds `slots`, so both are sized by it.
-size_t workspace_bytes_for(int slots) {
+constexpr size_t workspace_bytes_for(int slots) {
   return static_cast<size_t>(slots) *
          (kRowStride * sizeof(float) + kBwdWaves * kStashF4PerWave * sizeof(f4));
 }
+
+// Scratch of fhoad_forward_laplacian_backward_noalloc: a file-scope device array, one per GPU
+// (each device that loads this code object holds its own copy until the process ends). It is
+// sized for kMaxSlots slots, the most any batch uses (both gradient kernels cap their slots
+// at kMaxSlots), so every batch fits. Host code never passes `scratch` itself to a kernel:
+// the name is a host-side stand-in, and the device address comes from hipGetSymbolAddress
+// (noalloc_scratch below).
+constexpr size_t kNoAllocScratchBytes = workspace_bytes_for(kMaxSlots);
+static_assert(kNoAllocScratchBytes % sizeof(f4) == 0, "the scratch holds whole f4 stash entries");
+static __device__ __align__(256) f4 scratch[kNoAllocScratchBytes / sizeof(f4)];
 
 int64_t split_tiles(int64_t points) { return (points + kTile - 1) / kTile; }
 
@@ -2148,6 +2158,37 @@ int backward_grid(int slots, int* grid) {
   }
   return FHOAD_SUCCESS;
 }
+
+// Device address of this device's `scratch`, looked up once per device (with that device
+// current, on the first no-allocation call there) and kept per device: each GPU holds its own
+// copy of the array at its own address. The cache entries are atomic, so calls from several
+// host threads may fill one (with the same address).
+int noalloc_scratch(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> addresses[kMaxDevices] = {};
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return fail(FHOAD_ERROR_DEVICE, "hipGetDevice: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices) {
+    return fail(FHOAD_ERROR_DEVICE, "device %d is beyond the %d devices the scratch table covers",
+                device, kMaxDevices);
+  }
+  void* address = addresses[device].load(std::memory_order_acquire);
+  if (address == nullptr) {
+    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || address == nullptr) {
+      return fail(FHOAD_ERROR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(err));
+    }
+    addresses[device].store(address, std::memory_order_release);
+  }
+  *out = address;
+  return FHOAD_SUCCESS;
+}
+
+// Backward call on a workspace of `workspace_bytes` bytes (checked by the caller).
+int launch_backward(const float* coordinates, const float* parameters, const float* grad_output,
+                    const float* grad_laplacian, float* grad_parameters, float* grad_coordinates,
+                    void* workspace, int64_t batch, hipStream_t hs);
 
 }  // namespace
 }  // namespace fhoad
@@ -2244,6 +2285,45 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
                 needed);
   }
   if (int st = check_workspace_alignment(workspace)) return st;
+  return launch_backward(coordinates, parameters, grad_output, grad_laplacian, grad_parameters,
+                         grad_coordinates, workspace, batch, hs);
+}
+
+extern "C" int fhoad_forward_laplacian_backward_noalloc(
+    const float* coordinates, const float* parameters, const float* grad_output,
+    const float* grad_laplacian, float* grad_parameters, float* grad_coordinates, int64_t batch,
+    int version, void* stream) {
+  if (version < 1 || version > 6) {
+    return fail(FHOAD_ERROR_INVALID_VERSION, "backward version must be 1 to 6");
+  }
+  if (batch < 0) return fail(FHOAD_ERROR_INVALID_VALUE, "batch must be non-negative");
+  if (!parameters || !grad_parameters) return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (batch == 0) {
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((kParameterCount + 255) / 256), dim3(256), 0, hs,
+                       grad_parameters, static_cast<int64_t>(kParameterCount));
+    return check_launch("fill_zero_kernel");
+  }
+  if (!coordinates || !grad_output || !grad_laplacian || !grad_coordinates) {
+    return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
+  }
+  const size_t needed = fhoad_backward_workspace_size(batch);
+  if (needed > kNoAllocScratchBytes) {
+    return fail(FHOAD_ERROR_WORKSPACE, "batch %lld needs %zu bytes of scratch, the static scratch holds %zu",
+                static_cast<long long>(batch), needed, kNoAllocScratchBytes);
+  }
+  void* device_scratch = nullptr;
+  if (int st = noalloc_scratch(&device_scratch)) return st;
+  return launch_backward(coordinates, parameters, grad_output, grad_laplacian, grad_parameters,
+                         grad_coordinates, device_scratch, batch, hs);
+}
+
+namespace fhoad {
+namespace {
+
+int launch_backward(const float* coordinates, const float* parameters, const float* grad_output,
+                    const float* grad_laplacian, float* grad_parameters, float* grad_coordinates,
+                    void* workspace, int64_t batch, hipStream_t hs) {
   float* partials = static_cast<float*>(workspace);
   int slots = 0, grid = 0;
   if (use_split_backward(batch, 0)) {
@@ -2276,6 +2356,9 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
                      dim3(kReduceGroups * 64), 0, hs, partials, slots, grad_parameters);
   return check_launch("reduce_partials_kernel");
 }
+
+}  // namespace
+}  // namespace fhoad
 
 extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* source,
                                        int64_t batch, const float* boundary,

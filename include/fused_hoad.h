@@ -90,6 +90,25 @@ int fhoad_forward_laplacian_backward(const float* coordinates, const float* para
                                      int version, void* stream);
 
 /*
+ * fhoad_forward_laplacian_backward without a workspace argument: it allocates nothing (no
+ * hipMalloc, hipFree or allocating library call). Its scratch is a static device array inside
+ * the library, one copy per GPU, held from the library's load on that GPU until the process
+ * ends: 29,884,416 bytes (256 partial-row slots of 12,800 floats plus four 16 KB stashes
+ * each), the most the backward needs for any batch, so every batch fits (a need beyond it
+ * would be rejected with FHOAD_ERROR_WORKSPACE). Nothing in it has to start at zero. Every
+ * call on one GPU shares that GPU's scratch, which keeps the last call's contents: calls that
+ * overlap on one GPU (other streams, other host threads) race and must be serialized by the
+ * caller. Results are bitwise those of fhoad_forward_laplacian_backward.
+ *
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ */
+int fhoad_forward_laplacian_backward_noalloc(const float* coordinates, const float* parameters,
+                                             const float* grad_output, const float* grad_laplacian,
+                                             float* grad_parameters, float* grad_coordinates,
+                                             int64_t batch, int version, void* stream);
+
+/*
  * Bytes of device workspace fhoad_poisson_adam_step needs for `batch` interior and
  * `boundary_count` boundary points. 0 for batch <= 0 or boundary_count < 0.
  */

@@ -55,6 +55,7 @@ def test_header_declares_the_entry_points() -> None:
         "fhoad_backward_workspace_size",
         "fhoad_forward_laplacian",
         "fhoad_forward_laplacian_backward",
+        "fhoad_forward_laplacian_backward_noalloc",
         "fhoad_last_error",
         "fhoad_parameter_count",
         "fhoad_poisson_adam_step",

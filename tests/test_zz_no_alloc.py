@@ -1,0 +1,95 @@
+"""fhoad_forward_laplacian_backward_noalloc: the backward call with the library's static device
+scratch instead of a caller workspace.
+
+Called through the C ABI (ctypes) on consecutive calls of decreasing size, each checked bitwise
+against fhoad_forward_laplacian_backward on a torch-allocated workspace (the existing entry
+point the parity tests pin against the oracle), and once against the float64 oracle directly.
+The sizes cover both gradient kernels: a ragged large batch (whole rounds of 64-point tiles plus
+split 16-point tiles), whole rounds only, and the small-batch kernel. Every call on the GPU
+shares the one scratch array, so the later, smaller calls run on what the earlier ones left.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import assert_scaled_close
+from gpu_helpers import announce, coordinates, packed, require_gpu_extension, to_numpy64, upstream
+
+pytestmark = pytest.mark.gpu
+
+LIBRARY = Path(__file__).resolve().parents[1] / "expanded-gpu-optimization_amd" / "fused_hoad" / "libfused_hoad_hip.so"
+
+
+def _lib() -> ctypes.CDLL:
+    lib = ctypes.CDLL(str(LIBRARY))
+    vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    lib.fhoad_last_error.restype = ctypes.c_char_p
+    lib.fhoad_backward_workspace_size.restype = ctypes.c_size_t
+    lib.fhoad_backward_workspace_size.argtypes = [i64]
+    lib.fhoad_forward_laplacian_backward.restype = ci
+    lib.fhoad_forward_laplacian_backward.argtypes = [vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, i64, ci, vp]
+    lib.fhoad_forward_laplacian_backward_noalloc.restype = ci
+    lib.fhoad_forward_laplacian_backward_noalloc.argtypes = [vp, vp, vp, vp, vp, vp, i64, ci, vp]
+    return lib
+
+
+def test_noalloc_backward_matches_the_workspace_entry_point() -> None:
+    require_gpu_extension()
+    lib = _lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    p = packed(0)
+    for call, batch in enumerate((70001, 65536, 1000)):
+        announce(f"noalloc backward call {call}: batch={batch} vs fhoad_forward_laplacian_backward")
+        x = coordinates(batch, seed=40 + call)
+        gu, gl = upstream(batch, seed=40 + call)
+        gu, gl = gu.reshape(-1).contiguous(), gl.reshape(-1).contiguous()
+
+        ws_bytes = lib.fhoad_backward_workspace_size(batch)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+        want_p = torch.empty(12737, device="cuda")
+        want_x = torch.empty(batch, 2, device="cuda")
+        status = lib.fhoad_forward_laplacian_backward(
+            x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), want_p.data_ptr(),
+            want_x.data_ptr(), ws.data_ptr(), ws_bytes, batch, 6, stream)
+        assert status == 0, lib.fhoad_last_error()
+
+        got_p = torch.full((12737,), float("nan"), device="cuda")
+        got_x = torch.full((batch, 2), float("nan"), device="cuda")
+        status = lib.fhoad_forward_laplacian_backward_noalloc(
+            x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), got_p.data_ptr(),
+            got_x.data_ptr(), batch, 6, stream)
+        assert status == 0, lib.fhoad_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(got_p, want_p), f"call {call}: grad_parameters differ"
+        assert torch.equal(got_x, want_x), f"call {call}: grad_coordinates differ"
+
+        if batch == 1000:  # and against the float64 oracle, to the parity tests' bar
+            from oracle import jet
+
+            ep, ex = jet.backward(to_numpy64(p), to_numpy64(x), to_numpy64(gu), to_numpy64(gl))
+            assert_scaled_close(to_numpy64(got_p), ep, 1e-4, "grad_parameters vs oracle")
+            assert_scaled_close(to_numpy64(got_x), ex, 1e-4, "grad_coordinates vs oracle")
+
+
+def test_noalloc_backward_argument_errors_and_empty_batch() -> None:
+    require_gpu_extension()
+    announce("noalloc backward: version and batch errors, empty batch zero-fills")
+    lib = _lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.fhoad_forward_laplacian_backward_noalloc(None, None, None, None, None, None, 4, 7, stream) == 1
+    assert b"backward version must be 1 to 6" in lib.fhoad_last_error()
+    assert lib.fhoad_forward_laplacian_backward_noalloc(None, None, None, None, None, None, -1, 6, stream) == 2
+    p = packed(0)
+    gp = torch.full((12737,), 5.0, device="cuda")
+    status = lib.fhoad_forward_laplacian_backward_noalloc(
+        None, p.data_ptr(), None, None, gp.data_ptr(), None, 0, 6, stream)
+    assert status == 0, lib.fhoad_last_error()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(gp).item() == 0
+    assert np.all(to_numpy64(gp) == 0.0)
