@@ -169,27 +169,6 @@ __device__ __forceinline__ void tanh_jet_adjoint_vs(float v, float s, float zj0,
   bl = bls;
 }
 
-// tanh_jet_adjoint_vs for the output layer's seed, whose Jbar is zero (the output feeds only
-// u and the Laplacian), and with kZeroV also vbar = 0 (interior points of the fused step: the
-// loss has no u term there). It drops only operations on those zeros, so its results are the
-// general form's, up to the sign of an exact zero.
-template <bool kZeroV>
-__device__ __forceinline__ void tanh_jet_adjoint_seed(float v, float s, float zj0, float zj1,
-                                                      float zl, float& bv, float& bj0,
-                                                      float& bj1, float& bl) {
-  const float q = __builtin_fmaf(zj0, zj0, zj1 * zj1);
-  const float p = __builtin_fmaf(v, q, zl);
-  const float kv = kKappa * v;
-  const float bls = bl * s;
-  const float t = kZeroV ? kv * (bl * p) : __builtin_fmaf(kv, bl * p, bv);
-  const float nv = s * __builtin_fmaf(bls, q, t);
-  const float m2 = 2.0f * (bls * v);
-  bj0 = m2 * zj0;
-  bj1 = m2 * zj1;
-  bv = nv;
-  bl = bls;
-}
-
 // tanh_jet_adjoint_vs for layer 0, whose z_J are the W0 columns and z_L = 0: q = |z_J|^2 is
 // the per-neuron constant staged in kSmallQ0 (the same fma), and p = v q.
 __device__ __forceinline__ void tanh_jet_adjoint_layer0(float v, float s, float zj0, float zj1,
@@ -338,44 +317,6 @@ __device__ __forceinline__ float layer0_zv(const Layer0Weights& w, int r, float 
   return __builtin_fmaf(w.cwx[r], x0, __builtin_fmaf(w.cwy[r], x1, w.cb[r]));
 }
 
-// Hidden-layer product acc[mb][c] += W[16 mb + ., :] H[:, c, .] with H in registers (see the
-// header comment for the k-step assignment), for the backward's forward recompute: w points at
-// this lane's row base (68 m + 4 g) in the layer's pitch-68 plane, and one 16-byte read gives
-// the A operands of k-steps (ob, 0..3). The first k-step takes its C operand from `bias`
-// (value component) or zero, so no accumulator needs initialising.
-// The operands of block ob + 1 are read before the 64 MFMAs of block ob are issued, so the LDS
-// latency hides behind MFMA work.
-__device__ __forceinline__ void hidden_product(const float* w, const f4 (&h)[4][4],
-                                               const f4 (&bias)[4], f4 (&acc)[4][4]) {
-  f4 next[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) next[mb] = lds4(w + 1088 * mb);
-#pragma unroll
-  for (int ob = 0; ob < 4; ++ob) {
-    f4 a[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) a[mb] = next[mb];
-    if (ob < 3) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) next[mb] = lds4(w + 1088 * mb + 16 * (ob + 1));
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const f4 cin = (ob | j) ? acc[mb][c] : (c == 0 ? bias[mb] : f4{0.f, 0.f, 0.f, 0.f});
-          acc[mb][c] = mfma(a[mb][j], h[ob][c][j], cin);
-        }
-      }
-    }
-    // Schedule: the next block's four DS reads, then this block's 64 MFMAs.
-    if (ob < 3) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 64, 0);
-  }
-}
-
 // Forward hidden product with the operand-native weight layout: wa points at this lane's f4
 // in the layer's block; k-step (ob, j) reads wa[(4 ob + j) * 64]. Each k-step's operand is
 // read one k-step ahead, with a fence on both sides of the step's 16 MFMAs so the read stays
@@ -407,52 +348,10 @@ __device__ __forceinline__ void hidden_product_native(const f4* wa, const f4 (&h
   }
 }
 
-// Transposed product hb[ib][c] = sum_o W[o][16 ib + .] zb[o][c][.]: the adjoint of a hidden
-// layer's input. zb is in the same register layout as h; w points at this lane's column base.
-// The A operands of k-step n + 1 are read from LDS before the 16 MFMAs of k-step n are issued,
-// so the read latency hides behind MFMA work (one wave per SIMD has no other wave to switch to).
-__device__ __forceinline__ void hidden_product_t(const float* w, const f4 (&zb)[4][4],
-                                                 f4 (&hb)[4][4]) {
-  float next[4];
-#pragma unroll
-  for (int ib = 0; ib < 4; ++ib) next[ib] = w[16 * ib];
-#pragma unroll
-  for (int step = 0; step < 16; ++step) {
-    const int ob = step >> 2, j = step & 3;
-    float a[4];
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) a[ib] = next[ib];
-    if (step < 15) {
-      const int nob = (step + 1) >> 2, nj = (step + 1) & 3;
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib) next[ib] = w[1088 * nob + kWRow * nj + 16 * ib];
-    }
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const f4 cin = (ob | j) ? hb[ib][c] : f4{0.f, 0.f, 0.f, 0.f};
-        hb[ib][c] = mfma(a[ib], zb[ob][c][j], cin);
-      }
-    }
-    // Schedule: the next step's two DS reads, then this step's 16 MFMAs.
-    if (step < 15) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
-  }
-}
-
 // Scaled value biases c b of the 4 x 4 neurons 16 mb + 4 g + r held by this lane.
 __device__ __forceinline__ void load_bias(const float* s_small, int layer, int g, f4 (&bias)[4]) {
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) bias[mb] = lds4(s_small + kSmallBh + layer * kHidden + 16 * mb + 4 * g);
-}
-
-// acc = W_layer h + bias, for hidden layer `layer` (0..2) with w at this lane's row base.
-__device__ __forceinline__ void hidden_layer(const float* s_small, const float* w_rows, int layer,
-                                             int g, const f4 (&h)[4][4], f4 (&acc)[4][4]) {
-  f4 bias[4];
-  load_bias(s_small, layer, g, bias);
-  hidden_product(w_rows + layer * kPlane, h, bias, acc);
 }
 
 // tanh_jet over a layer's 16 values per lane, the tanh four at a time (tanh_scaled4).
@@ -469,27 +368,6 @@ __device__ __forceinline__ void apply_tanh_jet(const f4 (&z)[4][4], f4 (&h)[4][4
       h[mb][1][r] = sl[r] * zj0;
       h[mb][2][r] = sl[r] * zj1;
       h[mb][3][r] = sl[r] * __builtin_fmaf(v[r], q, z[mb][3][r]);
-    }
-  }
-}
-
-// apply_tanh_jet that also returns (v', s') of every value.
-__device__ __forceinline__ void apply_tanh_jet_vs(const f4 (&z)[4][4], f4 (&h)[4][4],
-                                                  f4 (&tv)[4], f4 (&ts)[4]) {
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    f4 v4, s4;
-    tanh_scaled4(z[mb][0], v4, s4);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = v4[r], sl = s4[r];
-      const float q = __builtin_fmaf(z[mb][1][r], z[mb][1][r], z[mb][2][r] * z[mb][2][r]);
-      h[mb][0][r] = v;
-      h[mb][1][r] = sl * z[mb][1][r];
-      h[mb][2][r] = sl * z[mb][2][r];
-      h[mb][3][r] = sl * __builtin_fmaf(v, q, z[mb][3][r]);
-      tv[mb][r] = v;
-      ts[mb][r] = sl;
     }
   }
 }
@@ -533,6 +411,13 @@ __device__ __forceinline__ T opaque(T x) {
 // the whole kernel. An empty asm statement with a memory clobber at the top of each tile keeps
 // them as per-tile LDS reads.
 __device__ __forceinline__ void keep_lds_reads_in_loop() { __asm__ volatile("" ::: "memory"); }
+
+// A scheduling fence that LDS accesses and MFMAs do not cross; VALU and SALU instructions may.
+// Placed between the LDS reads for the next step and the MFMAs of the current one, it keeps
+// the reads issued a step ahead (at full register use the scheduler otherwise sinks each read
+// to just before its first use, and the MFMA then waits out the LDS latency), while the
+// VALU work around them can still fill MFMA latencies.
+__device__ __forceinline__ void lds_mfma_fence() { __builtin_amdgcn_sched_barrier(0x0406); }
 
 // Value of lane l ^ 32 (permlane32) or l ^ 16 (permlane16) in every lane, with gfx950's
 // v_permlane32_swap / v_permlane16_swap (VALU, no LDS round trip). swap(u, 0) leaves the
@@ -815,10 +700,11 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
 //
 // One workgroup per CU, 4 waves (one per SIMD, up to 512 registers each), 64-point workgroup
 // tiles (16 points per wave). Per tile:
-//   1. every wave re-runs the forward for its 16 points, keeping the pre-activations z in
-//      registers (hidden layer 1's in a per-wave stash, see below);
+//   1. every wave re-runs the forward for its 16 points, keeping each hidden layer's tanh-jet
+//      output h in registers;
 //   2. the adjoint is seeded from the linear output layer and walked back through layers 3..1:
-//      tanh-jet adjoint in registers, dW += zbar h_prev^T, hbar = W^T zbar (registers), and
+//      tanh-jet adjoint from h in registers (tanh_jet_adjoint_h, no tanh re-evaluated),
+//      dW += zbar h_prev^T, hbar = W^T zbar one input block at a time (registers), and
 //      finally layer 0 in closed form;
 //   3. dW contracts over the points of all 4 waves: zbar and h_prev are staged in LDS (two
 //      components at a time) and wave w owns output rows 16 w .. 16 w + 15 of every dW; the
@@ -833,7 +719,6 @@ constexpr int kBwdWaves = 4;
 constexpr int kBwdTile = kBwdWaves * kTile;  // 64 points
 constexpr int kMaxSlots = 256;
 constexpr int kRowStride = 12800;            // floats per partial row (>= 12737)
-constexpr int kStashF4PerWave = 16 * kWave;  // hidden layer 1's z for one wave tile (16 KB)
 constexpr int kReduceGroups = 16;            // fixed reduction tree: 16 groups of 16 slots
 static_assert(kMaxSlots % kReduceGroups == 0, "reduction tree must tile the slots");
 
@@ -859,21 +744,32 @@ __device__ __forceinline__ void stage_write(float* stage_lane, int mb, int r, fl
 // plane 0 holds zbar_v).
 __device__ __forceinline__ float dw_product(const float* stage_rows, int w, f4 (&dw)[4]) {
   float bias = 0.0f;
+  // Steps (cc, s) in order; each step's five 16-byte operands are read one step ahead.
+  f4 na, nb[4];
+  na = lds4(stage_rows + 1088 * w);
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
+  for (int b = 0; b < 4; ++b) nb[b] = lds4(stage_rows + 2 * kPlane + 1088 * b);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const f4 a = lds4(stage_rows + cc * kPlane + 1088 * w + 16 * s);
-      f4 b[4];
+  for (int step = 0; step < 8; ++step) {
+    const int cc = step >> 2;
+    const f4 a = na;
+    f4 b[4];
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) b[nb] = lds4(stage_rows + (2 + cc) * kPlane + 1088 * nb + 16 * s);
+    for (int k = 0; k < 4; ++k) b[k] = nb[k];
+    if (step < 7) {
+      const int ncc = (step + 1) >> 2, ns = (step + 1) & 3;
+      na = lds4(stage_rows + ncc * kPlane + 1088 * w + 16 * ns);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (cc == 0) bias += a[k];
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) dw[nb] = mfma(a[k], b[nb][k], dw[nb]);
-      }
+      for (int k = 0; k < 4; ++k) nb[k] = lds4(stage_rows + (2 + ncc) * kPlane + 1088 * k + 16 * ns);
     }
+    lds_mfma_fence();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (cc == 0) bias += a[k];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) dw[n] = mfma(a[k], b[n][k], dw[n]);
+    }
+    lds_mfma_fence();
   }
   return bias;
 }
@@ -885,77 +781,27 @@ __device__ __forceinline__ float dw_product(const float* stage_rows, int w, f4 (
 // own the 64 neurons once each.
 __device__ __forceinline__ int owned_neuron(int m, int g) { return 16 * (m >> 2) + 4 * g + (m & 3); }
 
-// hidden layer 3's tanh_adjoint_in_place, from the output layer's seed (Jbar = 0, and with
-// kZeroV vbar = 0): tanh_jet_adjoint_seed.
-template <bool kZeroV>
-__device__ __forceinline__ void tanh_adjoint_seed_in_place(f4 (&z)[4][4], const f4 (&hb)[4][4],
-                                                           const f4 (&tv)[4], const f4 (&ts)[4]) {
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float bv = hb[mb][0][r], bj0 = 0.0f, bj1 = 0.0f, bl = hb[mb][3][r];
-      tanh_jet_adjoint_seed<kZeroV>(tv[mb][r], ts[mb][r], z[mb][1][r], z[mb][2][r], z[mb][3][r],
-                                    bv, bj0, bj1, bl);
-      z[mb][0][r] = bv;
-      z[mb][1][r] = bj0;
-      z[mb][2][r] = bj1;
-      z[mb][3][r] = bl;
-    }
-  }
-}
-
-// Replace a hidden layer's pre-activation z by its adjoint zbar, given the adjoint hb of the
-// layer's output and the layer's (v', s') from tanh_scaled4 (lane-local).
-__device__ __forceinline__ void tanh_adjoint_in_place(f4 (&z)[4][4], const f4 (&hb)[4][4],
-                                                      const f4 (&tv)[4], const f4 (&ts)[4]) {
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float bv = hb[mb][0][r], bj0 = hb[mb][1][r], bj1 = hb[mb][2][r], bl = hb[mb][3][r];
-      tanh_jet_adjoint_vs(tv[mb][r], ts[mb][r], z[mb][1][r], z[mb][2][r], z[mb][3][r], bv, bj0,
-                          bj1, bl);
-      z[mb][0][r] = bv;
-      z[mb][1][r] = bj0;
-      z[mb][2][r] = bj1;
-      z[mb][3][r] = bl;
-    }
-  }
-}
-
-// dW += zbar h_prev^T over the workgroup tile, in two passes of two jet components: (v, L)
-// first, then (J0, J1). h_prev, the tanh jet of zp, is rebuilt from the previous layer's
-// scaled pre-activation (or, with kFromLayer0, from layer 0's closed form
-// z' = (c (W0 x + b0), 2 W0[:,0], 2 W0[:,1], 0)); one tanh per value serves both passes, and
-// its (v', s') are returned in (pv, ps) for the previous layer's own adjoint. Adds the bias
-// gradient sum_p zbar_v' = sum_p zbar_v / c to g_bias.
-template <bool kFromLayer0>
-__device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&zp)[4][4],
-                                             f4 (&dw)[4], float& g_bias, float* stage_lane,
-                                             const float* stage_rows, const float* s_small,
-                                             int w, int g, float x0, float x1, f4 (&pv)[4],
-                                             f4 (&ps)[4]) {
+// dW1 += zbar1 h0^T over the workgroup tile, in two passes of two jet components: (v, L) first,
+// then (J0, J1). h0 is layer 0's output, rebuilt from its closed form
+// z' = (c (W0 x + b0), 2 W0[:,0], 2 W0[:,1], 0); its (v', s') are returned in (pv, ps) for
+// layer 0's own adjoint. Adds the bias gradient sum_p zbar_v' = sum_p zbar_v / c to g_bias.
+__device__ __forceinline__ void stage_and_dw_layer0(const f4 (&zbar)[4][4], f4 (&dw)[4],
+                                                    float& g_bias, float* stage_lane,
+                                                    const float* stage_rows, const float* s_small,
+                                                    int w, int g, float x0, float x1,
+                                                    f4 (&pv)[4], f4 (&ps)[4]) {
   __syncthreads();  // previous readers of the staging buffer are done
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
-    Layer0Weights w0;
-    if (kFromLayer0) w0 = layer0_weights(s_small, mb, g);
+    const Layer0Weights w0 = layer0_weights(s_small, mb, g);
     f4 zv;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) zv[r] = kFromLayer0 ? layer0_zv(w0, r, x0, x1) : zp[mb][0][r];
+    for (int r = 0; r < 4; ++r) zv[r] = layer0_zv(w0, r, x0, x1);
     tanh_scaled4(zv, pv[mb], ps[mb]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float v = pv[mb][r], sl = ps[mb][r];
-      float l;
-      if (kFromLayer0) {
-        l = sl * (v * w0.q[r]);
-      } else {
-        const float q = __builtin_fmaf(zp[mb][1][r], zp[mb][1][r], zp[mb][2][r] * zp[mb][2][r]);
-        l = sl * __builtin_fmaf(v, q, zp[mb][3][r]);
-      }
-      stage_write(stage_lane, mb, r, zbar[mb][0][r], zbar[mb][3][r], v, l);
+      const float v = pv[mb][r];
+      stage_write(stage_lane, mb, r, zbar[mb][0][r], zbar[mb][3][r], v, ps[mb][r] * (v * w0.q[r]));
     }
   }
   __syncthreads();
@@ -963,14 +809,183 @@ __device__ __forceinline__ void stage_and_dw(const f4 (&zbar)[4][4], const f4 (&
   __syncthreads();
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
-    Layer0Weights w0;
-    if (kFromLayer0) w0 = layer0_weights(s_small, mb, g);
+    const Layer0Weights w0 = layer0_weights(s_small, mb, g);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float zj0 = kFromLayer0 ? w0.wx[r] : zp[mb][1][r];
-      const float zj1 = kFromLayer0 ? w0.wy[r] : zp[mb][2][r];
-      stage_write(stage_lane, mb, r, zbar[mb][1][r], zbar[mb][2][r], ps[mb][r] * zj0,
-                  ps[mb][r] * zj1);
+      stage_write(stage_lane, mb, r, zbar[mb][1][r], zbar[mb][2][r], ps[mb][r] * w0.wx[r],
+                  ps[mb][r] * w0.wy[r]);
+    }
+  }
+  __syncthreads();
+  dw_product(stage_rows, w, dw);
+}
+
+// ---- the interior tiles of backward_kernel: the walk back from each layer's tanh-jet output ----
+//
+// The adjoint of the tanh jet (tanh_jet_adjoint_vs) needs s', z'_J and P = z'_L + v' q' only
+// in the products the jet's output already holds: h' = (v', s' z'_J0, s' z'_J1, s' P), so
+// s' z'_J = h'_J, s' P = h'_L and s'^2 q' = |h'_J|^2. With s' from v' alone,
+//   s' = 1/4 + (kappa / 2) v'^2      (v' = (c / 4) tanh z_v, kappa = -8 / c^2: (1 - tanh^2) / 4),
+// the adjoint is
+//   zbar_L' = s' Lbar',   zbar_Jd' = s' Jbar_d' + 2 Lbar' v' h'_Jd,
+//   zbar_v' = s' vbar' + kappa v' (Jbar' . h'_J + Lbar' h'_L) + Lbar' |h'_J|^2
+// (18 instructions per value). A tile therefore keeps each hidden layer's output h (which the
+// forward re-run produces anyway, and which the weight gradient of the layer above needs) and
+// evaluates no tanh in the walk back. Near |tanh| = 1, s' carries an absolute rounding of about
+// 3e-8, as 1 - a^2 does in the reference (/root/reference/csrc/fused_backward.cu:65-89).
+constexpr float kHalfKappa = 0.5f * kKappa;
+
+__device__ __forceinline__ void tanh_jet_adjoint_h(float v, float hj0, float hj1, float hl,
+                                                   float& bv, float& bj0, float& bj1, float& bl) {
+  const float hk = kHalfKappa * v;
+  const float s = __builtin_fmaf(hk, v, 0.25f);
+  const float kv = hk + hk;
+  const float lv2 = bl * (v + v);
+  const float dot = __builtin_fmaf(bj0, hj0, bj1 * hj1);
+  const float q = __builtin_fmaf(hj0, hj0, hj1 * hj1);
+  const float t = __builtin_fmaf(bl, hl, dot);
+  const float nv = __builtin_fmaf(bl, q, __builtin_fmaf(kv, t, s * bv));
+  bj0 = __builtin_fmaf(lv2, hj0, s * bj0);
+  bj1 = __builtin_fmaf(lv2, hj1, s * bj1);
+  bv = nv;
+  bl = s * bl;
+}
+
+// tanh_jet_adjoint_h for the output layer's seed: Jbar' = 0 and, with kZeroV (interior points
+// of the fused step), vbar' = 0; only operations on those zeros are dropped.
+template <bool kZeroV>
+__device__ __forceinline__ void tanh_jet_adjoint_h_seed(float v, float hj0, float hj1, float hl,
+                                                        float& bv, float& bj0, float& bj1,
+                                                        float& bl) {
+  const float hk = kHalfKappa * v;
+  const float s = __builtin_fmaf(hk, v, 0.25f);
+  const float kv = hk + hk;
+  const float lv2 = bl * (v + v);
+  const float q = __builtin_fmaf(hj0, hj0, hj1 * hj1);
+  const float t = bl * hl;
+  const float w = kZeroV ? kv * t : __builtin_fmaf(kv, t, s * bv);
+  bv = __builtin_fmaf(bl, q, w);
+  bj0 = lv2 * hj0;
+  bj1 = lv2 * hj1;
+  bl = s * bl;
+}
+
+// One hidden layer of the forward re-run, one output block at a time: z = W[16 mb + ., :] h_in
+// + b (the first k-step takes the bias as its C operand), then the block's tanh jet into
+// h_out[mb]. Each accumulator takes its k-steps (ob, j) in order (as in forward_kernel's
+// hidden_product_native); a block's tanh jet (VALU) and the next block's 64 MFMAs are independent,
+// so either can fill the other's latencies. The next block's four A operands (16-byte LDS
+// reads) are issued before this block's MFMAs, so no block waits for LDS. w_rows is this
+// lane's row base (68 m + 4 g).
+__device__ __forceinline__ void forward_layer(const float* s_small, const float* w_rows, int layer,
+                                              int g, const f4 (&hin)[4][4], f4 (&hout)[4][4]) {
+  f4 bias[4];
+  load_bias(s_small, layer, g, bias);
+  const float* w = w_rows + layer * kPlane;
+  f4 next[4];
+#pragma unroll
+  for (int ob = 0; ob < 4; ++ob) next[ob] = lds4(w + 16 * ob);
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    f4 a[4];
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) a[ob] = next[ob];
+    if (mb < 3) {
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) next[ob] = lds4(w + 1088 * (mb + 1) + 16 * ob);
+    }
+    lds_mfma_fence();
+    f4 z[4];
+#pragma unroll
+    for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f4 cin = (ob | j) ? z[c] : (c == 0 ? bias[mb] : zero4());
+          z[c] = mfma(a[ob][j], hin[ob][c][j], cin);
+        }
+      }
+    }
+    lds_mfma_fence();  // the next block's reads stay ahead of this block's MFMAs
+    tanh_jet4(z, hout[mb]);
+  }
+}
+
+// A operands of transposed_block for input block ib: W[16 ob + 4 g + j][16 ib + m] for the 16
+// k-steps (ob, j), 4-byte LDS reads from this lane's column base w (272 g + m) in the layer's
+// pitch-68 plane.
+__device__ __forceinline__ void transposed_operands(const float* w, int ib, float (&a)[16]) {
+#pragma unroll
+  for (int step = 0; step < 16; ++step) a[step] = w[1088 * (step >> 2) + kWRow * (step & 3) + 16 * ib];
+}
+
+// hb[c] = sum_o W[o][16 ib + .] zb[o][c][.] for one input block ib: 64 MFMAs over the k-steps
+// (ob, j) in order, from the operands a of
+// transposed_operands.
+__device__ __forceinline__ void transposed_block(const float (&a)[16], const f4 (&zb)[4][4],
+                                                 f4 (&hb)[4]) {
+#pragma unroll
+  for (int step = 0; step < 16; ++step) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      hb[c] = mfma(a[step], zb[step >> 2][c][step & 3], step ? hb[c] : zero4());
+    }
+  }
+}
+
+// The adjoint through one hidden layer's weights and the tanh jet below it, one input block at
+// a time: hbar = W^T zbar for block ib, then the tanh-jet adjoint of that block of the layer
+// below, from its output hp, which replaces hp[ib] by the layer below's zbar. Only one block of
+// hbar is live at a time.
+__device__ __forceinline__ void adjoint_through(const float* w, const f4 (&zb)[4][4],
+                                                f4 (&hp)[4][4]) {
+  float next[16];
+  transposed_operands(w, 0, next);
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib) {
+    float a[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a[k] = next[k];
+    if (ib < 3) transposed_operands(w, ib + 1, next);
+    lds_mfma_fence();
+    f4 hb[4];
+    transposed_block(a, zb, hb);
+    lds_mfma_fence();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
+      tanh_jet_adjoint_h(hp[ib][0][r], hp[ib][1][r], hp[ib][2][r], hp[ib][3][r], bv, bj0, bj1, bl);
+      hp[ib][0][r] = bv;
+      hp[ib][1][r] = bj0;
+      hp[ib][2][r] = bj1;
+      hp[ib][3][r] = bl;
+    }
+  }
+}
+
+// dW += zbar h_prev^T over the workgroup tile (stage_and_dw with h_prev given, not rebuilt):
+// two passes of two jet components, (v, L) then (J0, J1). Adds the bias gradient sum
+// sum_p zbar_v' to g_bias.
+__device__ __forceinline__ void stage_and_dw_h(const f4 (&zbar)[4][4], const f4 (&hp)[4][4],
+                                               f4 (&dw)[4], float& g_bias, float* stage_lane,
+                                               const float* stage_rows, int w) {
+  __syncthreads();  // previous readers of the staging buffer are done
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      stage_write(stage_lane, mb, r, zbar[mb][0][r], zbar[mb][3][r], hp[mb][0][r], hp[mb][3][r]);
+    }
+  }
+  __syncthreads();
+  g_bias += sum_lane_groups(dw_product(stage_rows, w, dw));
+  __syncthreads();
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      stage_write(stage_lane, mb, r, zbar[mb][1][r], zbar[mb][2][r], hp[mb][1][r], hp[mb][2][r]);
     }
   }
   __syncthreads();
@@ -1471,10 +1486,9 @@ __device__ __forceinline__ void split_tile(const float* s_w, const float* s_smal
   }
 }
 
-// z of hidden layers 2 and 3 stays in registers through the walk back; z of hidden layer 1
-// would push the live state past the register file, so each wave parks it in its own 16 KB
-// of the workspace (`stash`, coalesced 16-byte stores, L2-resident) and reloads it after
-// layer 3, into the registers layer 3's zbar leaves free.
+// The outputs h1, h2, h3 of the hidden layers stay in registers through the walk back (each
+// layer's zbar replaces its h in place, and hbar is live one 16-row block at a time), so no
+// layer is parked in memory.
 //
 // kLoss: grad_output and grad_laplacian are unused and the seed comes from `seed` (above);
 // grad_coordinates may be null.
@@ -1483,8 +1497,7 @@ __global__ void __launch_bounds__(kBwdWaves * kWave, 1)
 backward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                 const float* __restrict__ grad_output, const float* __restrict__ grad_laplacian,
                 float* __restrict__ grad_coordinates, float* __restrict__ partials,
-                f4* __restrict__ stash, int64_t batch, int64_t whole, int64_t tiles, int slots,
-                LossSeed seed) {
+                int64_t batch, int64_t whole, int64_t tiles, int slots, LossSeed seed) {
   constexpr int kStageFloats =
       kRest && kSplitScratchFloats > 4 * kPlane ? kSplitScratchFloats : 4 * kPlane;
   __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
@@ -1510,10 +1523,6 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   const int rows_off = lane_rows(m, g);
   const int cols_off = lane_cols(m, g);
   const int stage_lane_off = cols_off + 16 * w;
-  // This lane's slot in its wave's stash, as an offset from the kernel argument (an opaque
-  // pointer would lose its global address space and become flat accesses, which also hold up
-  // every LDS wait).
-  const int64_t stash_off = static_cast<int64_t>(blockIdx.x * kBwdWaves + w) * kStashF4PerWave + lane;
 
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
     WaveSums acc;
@@ -1553,27 +1562,15 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       float gu = kLoss ? 0.f : in.a, gl = kLoss ? 0.f : in.b;
       const float f = kLoss ? in.a : 0.f;
 
-      // ---- 1. forward recompute ----
-      f4 h[4][4];
-      f4 z2[4][4], z3[4][4];
-      layer0_forward(s_small, g, x0, x1, h);
+      // ---- 1. forward recompute, keeping each hidden layer's tanh-jet output ----
+      f4 h1[4][4], h2[4][4], h3[4][4];
       {
-        f4 z1[4][4];
-        hidden_layer(s_small, s_w + opaque(rows_off), 0, g, h, z1);
-        f4* stash_st = stash + opaque(stash_off);
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) stash_st[(4 * mb + c) * kWave] = z1[mb][c];
-        }
-        keep_lds_reads_in_loop();  // issue the stores here, so z1 is not held until later
-        apply_tanh_jet(z1, h);
+        f4 h0[4][4];
+        layer0_forward(s_small, g, x0, x1, h0);
+        forward_layer(s_small, s_w + opaque(rows_off), 0, g, h0, h1);
       }
-      hidden_layer(s_small, s_w + opaque(rows_off), 1, g, h, z2);
-      apply_tanh_jet(z2, h);
-      hidden_layer(s_small, s_w + opaque(rows_off), 2, g, h, z3);
-      f4 tv[4], ts[4];  // (v', s') of the layer whose adjoint comes next
-      apply_tanh_jet_vs(z3, h, tv, ts);
+      forward_layer(s_small, s_w + opaque(rows_off), 1, g, h1, h2);
+      forward_layer(s_small, s_w + opaque(rows_off), 2, g, h2, h3);
 
       if (kLoss) {
         // lap = w_out . L in the forward kernel's order, then the seed.
@@ -1582,7 +1579,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         for (int mb = 0; mb < 4; ++mb) {
           const f4 wo = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) out = __builtin_fmaf(wo[r], h[mb][3][r], out);
+          for (int r = 0; r < 4; ++r) out = __builtin_fmaf(wo[r], h3[mb][3][r], out);
         }
         out = sum_lane_groups(out);
         const float res = active ? out - f : 0.0f;
@@ -1590,14 +1587,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         acc.loss += sum_row16(res * res);
       }
 
-      // ---- 2. output layer: w_out / b_out gradients and the adjoint seed ----
+      // ---- 2. output layer: w_out / b_out gradients, and hidden layer 3's adjoint ----
       // In the scaled jet u = (4 w_out / c) . v' + b_out and lap = (4 w_out / lambda) . L', so
       // dw_out = sum_p (4 gu / c) v' + (4 gl / lambda) L' and the seeds are
       // vbar' = 4 gu w_out / c, Lbar' = 4 gl w_out / lambda, Jbar' = 0. The point sums stay in
-      // registers (row_reduce_scatter16).
-      // With kLoss, gu = 0 on interior points: the value seed and the u terms are dropped
-      // (their products with zero), which leaves the other results as they were.
-      f4 hb[4][4];
+      // registers (row_reduce_scatter16). With kLoss, gu = 0 on interior points: the value seed
+      // and the u terms are dropped (their products with zero). h3 becomes zbar3 in place.
       {
         const float gu_c = gu * (4.0f / kC);
         const float gl_l = gl * (4.0f / kLambda);
@@ -1608,68 +1603,68 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
           const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            wout_terms[4 * mb + r] = kLoss ? gl_l * h[mb][3][r]
-                                           : __builtin_fmaf(gu_c, h[mb][0][r], gl_l * h[mb][3][r]);
-            hb[mb][0][r] = kLoss ? 0.0f : gu * wv[r];
-            hb[mb][1][r] = 0.0f;
-            hb[mb][2][r] = 0.0f;
-            hb[mb][3][r] = gl * wl[r];
+            wout_terms[4 * mb + r] = kLoss ? gl_l * h3[mb][3][r]
+                                           : __builtin_fmaf(gu_c, h3[mb][0][r], gl_l * h3[mb][3][r]);
+            float bv = kLoss ? 0.0f : gu * wv[r], bj0, bj1, bl = gl * wl[r];
+            tanh_jet_adjoint_h_seed<kLoss>(h3[mb][0][r], h3[mb][1][r], h3[mb][2][r], h3[mb][3][r],
+                                           bv, bj0, bj1, bl);
+            h3[mb][0][r] = bv;
+            h3[mb][1][r] = bj0;
+            h3[mb][2][r] = bj1;
+            h3[mb][3][r] = bl;
           }
         }
         acc.wout += row_reduce_scatter16(wout_terms, m_pick);
         if (!kLoss) acc.bout += sum_row16(gu);
       }
 
-      // ---- 3. hidden layer 3 ----
-      tanh_adjoint_seed_in_place<kLoss>(z3, hb, tv, ts);
-      stage_and_dw<false>(z3, z2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
-                          s_stage + opaque(rows_off), s_small, w, g, x0, x1,
-                          tv, ts);
-      hidden_product_t(s_w + opaque(cols_off) + 2 * kPlane, z3, hb);
+      // ---- 3. hidden layer 3: dW3 from (zbar3, h2), then W3^T zbar3 into layer 2's adjoint ----
+      stage_and_dw_h(h3, h2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
+                     s_stage + opaque(rows_off), w);
+      adjoint_through(s_w + opaque(cols_off) + 2 * kPlane, h3, h2);
 
-      // ---- 4. hidden layer 2 (needs hidden layer 1's z back from the stash) ----
-      keep_lds_reads_in_loop();  // the reload below must read memory, not forward the stores
-      const f4* stash_ld = stash + opaque(stash_off);
-      f4 z1[4][4];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) z1[mb][c] = stash_ld[(4 * mb + c) * kWave];
-      }
-      tanh_adjoint_in_place(z2, hb, tv, ts);
-      stage_and_dw<false>(z2, z1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
-                          s_stage + opaque(rows_off), s_small, w, g, x0, x1,
-                          tv, ts);
-      deliver(next);  // the stash reload above has been waited for, and so has this
-      hidden_product_t(s_w + opaque(cols_off) + kPlane, z2, hb);
+      // ---- 4. hidden layer 2: dW2 from (zbar2, h1), then W2^T zbar2 into layer 1's adjoint ----
+      stage_and_dw_h(h2, h1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
+                     s_stage + opaque(rows_off), w);
+      deliver(next);  // the next tile's inputs, before this tile's stores
+      adjoint_through(s_w + opaque(cols_off) + kPlane, h2, h1);
 
-      // ---- 5. hidden layer 1 ----
-      tanh_adjoint_in_place(z1, hb, tv, ts);
-      stage_and_dw<true>(z1, z1, acc.dw[0], acc.bh[0], s_stage + opaque(stage_lane_off),
-                          s_stage + opaque(rows_off), s_small, w, g, x0, x1,
-                         tv, ts);
-      hidden_product_t(s_w + opaque(cols_off), z1, hb);
+      // ---- 5. hidden layer 1: dW1 from (zbar1, h0), h0 rebuilt with its (v', s') ----
+      f4 v0[4], s0[4];
+      stage_and_dw_layer0(h1, acc.dw[0], acc.bh[0], s_stage + opaque(stage_lane_off),
+                          s_stage + opaque(rows_off), s_small, w, g, x0, x1, v0, s0);
 
-      // ---- 6. layer 0 in closed form ----
+      // ---- 6. W1^T zbar1, one block at a time, into layer 0 in closed form ----
       // bv is the adjoint of z'_v = c z_v and bj_d that of z'_Jd = 2 W0[:, d], so
       // grad_x = (c W0)^T bv, dW0[o][d] = sum_p bv (c x_d) + 2 bj_d = 2 sum_p (bv (c x_d / 2) + bj_d)
       // (the row takes the 2), db0 = c sum_p bv.
       {
         float gx0 = 0.f, gx1 = 0.f, tx[16], ty[16], tb[16];
         const float cx0 = kHalfC * x0, cx1 = kHalfC * x1;
+        const float* w_t = s_w + opaque(cols_off);
+        float next_a[16];
+        transposed_operands(w_t, 0, next_a);
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const Layer0Weights w0 = layer0_weights(s_small, mb, g);
+        for (int ib = 0; ib < 4; ++ib) {
+          float a[16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) a[k] = next_a[k];
+          if (ib < 3) transposed_operands(w_t, ib + 1, next_a);
+          lds_mfma_fence();
+          f4 hb[4];
+          transposed_block(a, h1, hb);
+          lds_mfma_fence();
+          const Layer0Weights w0 = layer0_weights(s_small, ib, g);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float bv = hb[mb][0][r], bj0 = hb[mb][1][r], bj1 = hb[mb][2][r], bl = hb[mb][3][r];
-            tanh_jet_adjoint_layer0(tv[mb][r], ts[mb][r], w0.wx[r], w0.wy[r], w0.q[r], bv, bj0,
+            float bv = hb[0][r], bj0 = hb[1][r], bj1 = hb[2][r], bl = hb[3][r];
+            tanh_jet_adjoint_layer0(v0[ib][r], s0[ib][r], w0.wx[r], w0.wy[r], w0.q[r], bv, bj0,
                                     bj1, bl);
             gx0 = __builtin_fmaf(w0.cwx[r], bv, gx0);
             gx1 = __builtin_fmaf(w0.cwy[r], bv, gx1);
-            tx[4 * mb + r] = __builtin_fmaf(bv, cx0, bj0);  // dW0[o][0] / 2
-            ty[4 * mb + r] = __builtin_fmaf(bv, cx1, bj1);  // dW0[o][1] / 2
-            tb[4 * mb + r] = bv;                            // db0[o] / c
+            tx[4 * ib + r] = __builtin_fmaf(bv, cx0, bj0);  // dW0[o][0] / 2
+            ty[4 * ib + r] = __builtin_fmaf(bv, cx1, bj1);  // dW0[o][1] / 2
+            tb[4 * ib + r] = bv;                            // db0[o] / c
           }
         }
         acc.w0x += row_reduce_scatter16(tx, m_pick);
@@ -2075,7 +2070,7 @@ int current_device_cus(int* cus) {
   return FHOAD_SUCCESS;
 }
 
-// The stash part of the workspace is read and written as 16-byte vectors.
+// The workspace must be 16-byte aligned (part of the ABI: hipMalloc and torch allocations are).
 int check_workspace_alignment(const void* workspace) {
   if (reinterpret_cast<uintptr_t>(workspace) % alignof(f4) != 0) {
     return fail(FHOAD_ERROR_MISALIGNED, "workspace must be 16-byte aligned");
@@ -2089,11 +2084,9 @@ int slots_for_tiles(int64_t tiles) { return static_cast<int>(std::min<int64_t>(t
 
 int backward_slots(int64_t batch) { return slots_for_tiles(backward_tiles(batch)); }
 
-// Workspace of the gradient kernel for `slots` slots: the partial rows, then one z stash per
-// (workgroup, wave); the grid never exceeds `slots`, so both are sized by it.
+// Workspace of the gradient kernels for `slots` slots: one partial row per slot.
 constexpr size_t workspace_bytes_for(int slots) {
-  return static_cast<size_t>(slots) *
-         (kRowStride * sizeof(float) + kBwdWaves * kStashF4PerWave * sizeof(f4));
+  return static_cast<size_t>(slots) * kRowStride * sizeof(float);
 }
 
 // Scratch of fhoad_forward_laplacian_backward_noalloc: a file-scope device array, one per GPU
@@ -2103,8 +2096,8 @@ constexpr size_t workspace_bytes_for(int slots) {
 // the name is a host-side stand-in, and the device address comes from hipGetSymbolAddress
 // (noalloc_scratch below).
 constexpr size_t kNoAllocScratchBytes = workspace_bytes_for(kMaxSlots);
-static_assert(kNoAllocScratchBytes % sizeof(f4) == 0, "the scratch holds whole f4 stash entries");
-static __device__ __align__(256) f4 scratch[kNoAllocScratchBytes / sizeof(f4)];
+static_assert(kNoAllocScratchBytes % sizeof(float) == 0, "the scratch holds whole partial rows");
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
 int64_t split_tiles(int64_t points) { return (points + kTile - 1) / kTile; }
 
@@ -2133,15 +2126,12 @@ bool use_split_backward(int64_t batch, int64_t boundary_count) {
   return split_tiles(batch) + split_tiles(boundary_count) <= kSplitBwdMaxTiles;
 }
 
-// Workspace for either gradient kernel: the larger of backward_kernel's (partial rows and
-// stashes) and backward_split_kernel's (partial rows).
+// Workspace for either gradient kernel: one partial row per slot, for the larger slot count of
+// the two (a knob can force either kernel).
 size_t gradient_workspace_bytes(int64_t batch, int64_t boundary_count) {
-  const size_t tiled = workspace_bytes_for(
-      slots_for_tiles(backward_tiles(batch) + split_tiles(boundary_count)));
-  const size_t split =
-      static_cast<size_t>(slots_for_tiles(split_tiles(batch) + split_tiles(boundary_count))) *
-      kRowStride * sizeof(float);
-  return std::max(tiled, split);
+  const int64_t boundary_tiles = split_tiles(boundary_count);
+  return workspace_bytes_for(slots_for_tiles(
+      std::max(backward_tiles(batch), split_tiles(batch)) + boundary_tiles));
 }
 
 // Persistent grid of the gradient kernel: one workgroup per CU, at most one per slot.
@@ -2338,16 +2328,15 @@ int launch_backward(const float* coordinates, const float* parameters, const flo
     slots = backward_slots(batch);
     if (int st = backward_grid(slots, &grid)) return st;
     const InteriorTiles it = interior_tiles_for(batch, slots);
-    f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
     if (it.whole != it.total) {
       hipLaunchKernelGGL((backward_kernel<false, true>), dim3(grid), dim3(kBwdWaves * kWave), 0,
                          hs, coordinates, parameters, grad_output, grad_laplacian,
-                         grad_coordinates, partials, stash, batch, it.whole, it.total, slots,
+                         grad_coordinates, partials, batch, it.whole, it.total, slots,
                          LossSeed{});
     } else {
       hipLaunchKernelGGL((backward_kernel<false, false>), dim3(grid), dim3(kBwdWaves * kWave), 0,
                          hs, coordinates, parameters, grad_output, grad_laplacian,
-                         grad_coordinates, partials, stash, batch, it.whole, it.total, slots,
+                         grad_coordinates, partials, batch, it.whole, it.total, slots,
                          LossSeed{});
     }
     if (int st = check_launch("backward_kernel")) return st;
@@ -2409,15 +2398,14 @@ extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* so
                        batch, tiles, slots, seed);
     if (int st = check_launch("backward_split_kernel")) return st;
   } else {
-    f4* stash = reinterpret_cast<f4*>(partials + static_cast<size_t>(slots) * kRowStride);
     if (it.whole != it.total) {
       hipLaunchKernelGGL((backward_kernel<true, true>), dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
                          coordinates, parameters, nullptr, nullptr, grad_coordinates, partials,
-                         stash, batch, it.whole, tiles, slots, seed);
+                         batch, it.whole, tiles, slots, seed);
     } else {
       hipLaunchKernelGGL((backward_kernel<true, false>), dim3(grid), dim3(kBwdWaves * kWave), 0,
                          hs, coordinates, parameters, nullptr, nullptr, grad_coordinates,
-                         partials, stash, batch, it.whole, tiles, slots, seed);
+                         partials, batch, it.whole, tiles, slots, seed);
     }
     if (int st = check_launch("backward_kernel")) return st;
   }

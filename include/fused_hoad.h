@@ -63,9 +63,9 @@ int fhoad_forward_laplacian(const float* coordinates, const float* parameters, f
                             float* laplacian, int64_t batch, int version, void* stream);
 
 /*
- * Bytes of device workspace fhoad_forward_laplacian_backward needs for `batch` points
- * (per-slot weight-gradient partial rows, plus per-wave stashes for large batches). It depends
- * only on the batch. 0 for batch <= 0.
+ * Bytes of device workspace fhoad_forward_laplacian_backward needs for `batch` points: one
+ * weight-gradient partial row of 12,800 floats per slot, at most 256 slots (13,107,200 bytes).
+ * It depends only on the batch. 0 for batch <= 0.
  */
 size_t fhoad_backward_workspace_size(int64_t batch);
 
@@ -93,9 +93,9 @@ int fhoad_forward_laplacian_backward(const float* coordinates, const float* para
  * fhoad_forward_laplacian_backward without a workspace argument: it allocates nothing (no
  * hipMalloc, hipFree or allocating library call). Its scratch is a static device array inside
  * the library, one copy per GPU, held from the library's load on that GPU until the process
- * ends: 29,884,416 bytes (256 partial-row slots of 12,800 floats plus four 16 KB stashes
- * each), the most the backward needs for any batch, so every batch fits (a need beyond it
- * would be rejected with FHOAD_ERROR_WORKSPACE). Nothing in it has to start at zero. Every
+ * ends: 13,107,200 bytes (256 partial-row slots of 12,800 floats), the most the backward
+ * needs for any batch, so every batch fits (a need beyond it would be rejected with
+ * FHOAD_ERROR_WORKSPACE). Nothing in it has to start at zero. Every
  * call on one GPU shares that GPU's scratch, which keeps the last call's contents: calls that
  * overlap on one GPU (other streams, other host threads) race and must be serialized by the
  * caller. Results are bitwise those of fhoad_forward_laplacian_backward.

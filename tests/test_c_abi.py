@@ -80,11 +80,10 @@ def test_constants_and_status_strings() -> None:
 
 def _expected_workspace(batch: int, boundary: int = 0) -> int:
     """Either gradient kernel may run (a knob can force either), so the workspace covers the
-    larger need: 64-point interior tiles and 16-point boundary tiles with a partial row and
-    four 16 KB wave stashes per slot, or 16-point tiles with a partial row per slot; at most
-    256 slots."""
+    larger slot count: 64-point interior tiles or 16-point tiles, plus 16-point boundary
+    tiles, one partial row of 12,800 floats per slot, at most 256 slots."""
     row = 12800 * 4
-    tiled = min(256, -(-batch // 64) - (-boundary // 16)) * (row + 4 * 16 * 1024)
+    tiled = min(256, -(-batch // 64) - (-boundary // 16)) * row
     split = min(256, -(-batch // 16) - (-boundary // 16)) * row
     return max(tiled, split)
 
@@ -92,7 +91,7 @@ def _expected_workspace(batch: int, boundary: int = 0) -> int:
 def test_workspace_size_covers_either_gradient_kernel() -> None:
     lib = _lib()
     assert lib.fhoad_backward_workspace_size(0) == 0
-    per_slot = 12800 * 4 + 4 * 16 * 1024
+    per_slot = 12800 * 4
     assert lib.fhoad_backward_workspace_size(1) == per_slot
     assert lib.fhoad_backward_workspace_size(65536) == 256 * per_slot
     assert lib.fhoad_backward_workspace_size(1 << 20) == 256 * per_slot
