@@ -497,15 +497,46 @@ __device__ __forceinline__ float row_reduce_scatter16(const float (&v)[16], int 
 // ---------------------------------------------------------------------------------------------
 // Forward kernel (replaces fused_forward_laplacian_tiled_kernel<2>,
 // /root/reference/csrc/fused_residual.cu:157-295). A grid of at most one workgroup per CU
-// stages the weights once, then every wave walks 16-point tiles: tile t goes to workgroup
-// t % grid, wave (t / grid) % kWaves, so small batches still spread over all CUs.
+// stages the weights once, then every wave walks 16-point tiles: tile t < whole goes to
+// workgroup t % grid, wave (t / grid) % kWaves, so small batches still spread over all CUs.
+//
+// `whole` is a multiple of 4 x grid (one tile per SIMD per round), so every SIMD runs the same
+// number of whole tiles. The tiles past the last whole round (`split` tiles, fewer than one per
+// SIMD) would each add a whole tile's time to the SIMD that got it; instead, the last four
+// waves of each workgroup (one per SIMD, the ones with the fewest whole tiles) run them with a
+// 16-point tile's rows split between them, forward_split_kernel's decomposition: wave q
+// computes rows 16 q .. 16 q + 15 of every layer (64 MFMAs per layer instead of 256) and the
+// layer outputs go to the other three through LDS. The four meet at an LDS counter
+// (quad_sync), not at s_barrier, which would wait for the workgroup's waves still on whole
+// tiles. A split tile's chains are a whole tile's accumulators (mb = q, c) with the same
+// operands in the same order, so both paths give bitwise the same results.
+constexpr int kQuadSpinLimit = 1 << 24;  // about 0.5 s of s_sleep(1); never reached by a whole quad
+
+// The four waves of a quad each add 1 to `flag` per meeting and wait until it reaches `target`
+// (4 x the meetings so far). The release fence completes the wave's LDS writes before its
+// arrival; the acquire fence orders its later reads after the others' arrivals. Every quad wave
+// takes the same split tiles and meetings, so the wait ends; the spin limit only bounds it.
+__device__ __forceinline__ void quad_sync(unsigned* flag, unsigned target) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  for (int spin = 0; spin < kQuadSpinLimit; ++spin) {
+    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
 template <int kWaves>
 __global__ void __launch_bounds__(kWaves * kWave)
 forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                float* __restrict__ output, float* __restrict__ laplacian, int64_t batch,
-               int64_t tiles) {
+               int64_t whole, int64_t tiles) {
   __shared__ __attribute__((aligned(16))) float s_wa[3 * kOperandLayerF4 * 4];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
+  __shared__ f4 s_x[2][4][4][kWave];  // split tiles: [buffer][wave q][component][lane], 32 KB
+  __shared__ unsigned s_quad;         // split tiles: quad_sync counter
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int g = lane >> 4;
@@ -515,24 +546,98 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
   // waits for global memory; a wave that runs alone on its SIMD would expose that latency.
   int64_t tile = blockIdx.x + static_cast<int64_t>(wave) * gridDim.x;
   float next_x0 = 0.0f, next_x1 = 0.0f;
-  if (tile * kTile + m < batch) {
+  if (tile < whole && tile * kTile + m < batch) {
     next_x0 = coordinates[2 * (tile * kTile + m)];
     next_x1 = coordinates[2 * (tile * kTile + m) + 1];
   }
+  if (threadIdx.x == 0) s_quad = 0;
   stage_operand_weights<kWaves * kWave>(params, s_wa, threadIdx.x);
   stage_small(params, s_small, threadIdx.x, kWaves * kWave);
   __syncthreads();
   next_x0 = opaque(next_x0);  // delivered before the loop, for the same reason as below
   next_x1 = opaque(next_x1);
 
+  // ---- split tiles first: the last four waves, one 16-point tile at a time, rows split ----
+  // (first, so their quarter tiles interleave with the other waves' whole tiles on each SIMD)
+  const int q = wave - (kWaves - 4);
+  if (q >= 0 && whole < tiles) {
+    const float* wa_q = s_wa + 4 * lane + q;  // component q of this lane's operand f4s
+    unsigned meetings = 0;
+    int phase = 0;  // alternates the exchange buffers across layers and tiles
+    for (int64_t t = whole + blockIdx.x; t < tiles; t += gridDim.x) {
+      keep_lds_reads_in_loop();
+      const int64_t point = t * kTile + m;
+      const bool active = point < batch;
+      float x0 = 0.0f, x1 = 0.0f;
+      if (active) {
+        x0 = coordinates[2 * point];
+        x1 = coordinates[2 * point + 1];
+      }
+      f4 h[4][4];
+      layer0_forward(s_small, g, x0, x1, h);
+#pragma unroll
+      for (int layer = 0; layer < 3; ++layer) {
+        const f4 bias = lds4(s_small + kSmallBh + layer * kHidden + 16 * q + 4 * g);
+        f4 acc[4];
+#pragma unroll
+        for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // 4 W[16 q + m][16 ob + 4 g + j]: component q of k-step (ob, j)'s operand f4
+            const float a = wa_q[4 * ((16 * layer + 4 * ob + j) * kWave)];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const f4 cin = (ob | j) ? acc[c] : (c == 0 ? bias : f4{0.f, 0.f, 0.f, 0.f});
+              acc[c] = mfma(a, h[ob][c][j], cin);
+            }
+          }
+        }
+        f4 mine[4];
+        tanh_jet4(acc, mine);
+        f4 (*buf)[4][kWave] = s_x[phase];
+        phase ^= 1;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) buf[q][c][lane] = mine[c];
+        meetings += 4;
+        quad_sync(&s_quad, meetings);
+        if (layer < 2 || q == 0) {  // after the last layer only wave q = 0 (the output) reads
+#pragma unroll
+          for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) h[ob][c] = buf[ob][c][lane];
+          }
+        }
+      }
+      if (q == 0) {
+        float u = 0.0f, lap = 0.0f;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+          const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            u = __builtin_fmaf(wv[r], h[mb][0][r], u);
+            lap = __builtin_fmaf(wl[r], h[mb][3][r], lap);
+          }
+        }
+        u = sum_lane_groups(u);
+        lap = sum_lane_groups(lap);
+        if (g == 0 && active) {
+          output[point] = u + s_small[kSmallBout];
+          laplacian[point] = lap;
+        }
+      }
+    }
+  }
+
   const f4* wa_lane = reinterpret_cast<const f4*>(s_wa) + lane;
-  for (; tile < tiles; tile += step) {
+  for (; tile < whole; tile += step) {
     keep_lds_reads_in_loop();
     const int64_t point = tile * kTile + m;
     const bool active = point < batch;
     const float x0 = next_x0, x1 = next_x1;
     const int64_t next_point = (tile + step) * kTile + m;
-    if (next_point < batch) {
+    if (tile + step < whole && next_point < batch) {
       next_x0 = coordinates[2 * next_point];
       next_x1 = coordinates[2 * next_point + 1];
     }
@@ -571,6 +676,7 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
       laplacian[point] = lap;
     }
   }
+
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2044,6 +2150,19 @@ int check_launch(const char* what) {
   return FHOAD_SUCCESS;
 }
 
+// Tiles of forward_kernel that run whole: all of them below one round of one tile per SIMD
+// (4 per workgroup) or when the rounds are whole, otherwise the whole rounds; the rest run as
+// split tiles. FUSED_HOAD_FWD_SPLIT_REST=0 (experiment knob, read per call) runs every tile
+// whole.
+int64_t forward_whole_tiles(int64_t tiles, int grid) {
+  const int64_t round = 4 * static_cast<int64_t>(grid);
+  if (const char* env = std::getenv("FUSED_HOAD_FWD_SPLIT_REST")) {
+    if (std::atoi(env) == 0) return tiles;
+  }
+  if (tiles < round || tiles % round == 0) return tiles;
+  return tiles - tiles % round;
+}
+
 // Compute units of the current device, queried once per device. The cache entries are atomic:
 // calls from several host threads may fill the same entry (with the same value).
 int current_device_cus(int* cus) {
@@ -2227,14 +2346,15 @@ extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* pa
                        coordinates, parameters, output, laplacian, batch, tiles);
     return check_launch("forward_split_kernel");
   }
+  const int64_t whole = forward_whole_tiles(tiles, grid);
   // FUSED_HOAD_FWD_WAVES=8 (experiment knob, read per call) selects 8 waves per workgroup.
   const char* env = std::getenv("FUSED_HOAD_FWD_WAVES");
   if (env && std::atoi(env) == 8) {
     hipLaunchKernelGGL(forward_kernel<8>, dim3(grid), dim3(8 * kWave), 0, hs, coordinates,
-                       parameters, output, laplacian, batch, tiles);
+                       parameters, output, laplacian, batch, whole, tiles);
   } else {
     hipLaunchKernelGGL(forward_kernel<kFwdWaves>, dim3(grid), dim3(kFwdWaves * kWave), 0, hs,
-                       coordinates, parameters, output, laplacian, batch, tiles);
+                       coordinates, parameters, output, laplacian, batch, whole, tiles);
   }
   return check_launch("forward_kernel");
 }

@@ -33,7 +33,9 @@ def _fused(x, p, version=2):
 # the reference's tile edges (test_fused.py:28) plus this kernel's: 16-point wave tiles, and
 # ragged large batches (a partial last tile, workgroups with unequal tile counts)
 @pytest.mark.parametrize(
-    "batch", [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 4097, 16384, 65536, 65537, 262145]
+    "batch",
+    [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 4097, 16384, 16401, 65536, 65537, 70000,
+     100000, 262145],
 )
 def test_forward_matches_torch_forward_laplacian(batch: int) -> None:
     announce(f"forward vs torch forward Laplacian, batch={batch}")
@@ -121,6 +123,30 @@ def test_split_forward_is_bitwise_equal_to_the_tiled_kernel(batch: int, scale: f
         u_split, l_split = _fused(x, p)
     torch.cuda.synchronize()
     assert torch.equal(u_tiled, u_split) and torch.equal(l_tiled, l_split)
+
+
+@pytest.mark.parametrize(
+    "batch,scale,waves",
+    [(16401, 1.0, "12"), (65537, 1.0, "12"), (70000, 3.0, "12"), (100000, 1.0, "12"),
+     (262145, 1.0, "12"), (70000, 1.0, "8")],
+)
+def test_forward_split_rest_is_bitwise_equal_to_whole_tiles(batch: int, scale: float, waves: str) -> None:
+    """Past the last whole round (one 16-point tile per SIMD), the tiled kernel runs the
+    remaining tiles with their rows split over each workgroup's last four waves, which meet at
+    an LDS counter; FUSED_HOAD_FWD_SPLIT_REST=0 runs them as whole tiles. The split tiles run
+    the whole tiles' MFMA chains and tanh updates in the same order, so the outputs are bitwise
+    equal. 16,401 points leave two split tiles after one round; 70,000 points put two split
+    tiles on some workgroups (two passes through both exchange buffers); scale 3 saturates the
+    tanh; 8-wave workgroups use waves 4-7 as the quad."""
+    announce(f"forward split rest tiles vs whole tiles, batch={batch}, weights x{scale}, waves={waves}")
+    p = packed(0) * scale
+    x = coordinates(batch, seed=29)
+    with knobs(FUSED_HOAD_FWD_WAVES=waves, FUSED_HOAD_FWD_SPLIT="0"):
+        u_split, l_split = _fused(x, p)
+        with knobs(FUSED_HOAD_FWD_SPLIT_REST="0"):
+            u_whole, l_whole = _fused(x, p)
+    torch.cuda.synchronize()
+    assert torch.equal(u_split, u_whole) and torch.equal(l_split, l_whole)
 
 
 def test_forward_handles_empty_batch() -> None:
