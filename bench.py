@@ -9,8 +9,10 @@ input coordinates): ``train_step_ms`` is the fused step (FusedPoissonAdam: one g
 that re-runs the forward and seeds itself from the loss, one reduction kernel with the Adam
 update), ``train_step_graphed_ms`` the same replayed from a HIP graph, and
 ``train_step_autograd_ms`` the reference's step through the drop-in API (fused forward +
-autograd loss + fused backward + torch.optim.Adam). ``train_step_no_coordinate_grad_ms`` is
-the fused step without the coordinate gradient, a labelled variant only.
+autograd loss + fused backward + torch.optim.Adam) on a model flattened once with
+``flatten_poisson_parameters_`` (``train_step_autograd_unflattened_ms``: on the model as
+built). ``train_step_no_coordinate_grad_ms`` is the fused step without the coordinate
+gradient, a labelled variant only.
 
 ``roofline.traffic`` comes from the committed rocprofv3 summary
 profiles/forward_kernel_65536_traffic.json only when that was measured on the kernel source
@@ -185,7 +187,7 @@ def main() -> None:
         load_extension,
     )
     from fused_hoad.backends.fused import _recompute_backward, fused_laplacian
-    from fused_hoad.parameters import pack_poisson_parameters
+    from fused_hoad.parameters import flatten_poisson_parameters_, pack_poisson_parameters
     from fused_hoad.training import FusedPoissonAdam
 
     load_extension()  # fail loudly if the HIP extension is missing
@@ -252,21 +254,34 @@ def main() -> None:
 
     # ---- training step (a): the reference's step through the drop-in API ----
     # fused forward (autograd.Function) + mean((Lap u - f)^2) + fused backward + torch Adam
-    # (/root/reference/benchmarks/benchmark_training.py:41-60).
-    optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)
+    # (/root/reference/benchmarks/benchmark_training.py:41-60). train_step_autograd_ms runs it
+    # on a model flattened once with flatten_poisson_parameters_ (its parameters become views
+    # of the packed buffer, so fused_laplacian packs nothing per step);
+    # train_step_autograd_unflattened_ms on the model as built (a torch.cat pack per step).
     source = manufactured_source(x_train)
 
-    def autograd_step():
-        optimizer.zero_grad(set_to_none=True)
-        _, lap_t = fused_laplacian(model, x_train)
-        (lap_t - source).pow(2).mean().backward()
-        optimizer.step()
+    def autograd_timing(flatten: bool) -> float:
+        torch.manual_seed(0)
+        step_model = build_mlp(DEFAULT_POISSON_MLP).to(device)
+        if flatten:
+            flatten_poisson_parameters_(step_model)
+        optimizer = torch.optim.Adam(step_model.parameters(), lr=1e-3)
 
-    for _ in range(args.warmup):
-        autograd_step()
-    autograd_total_ms, _ = _timed(autograd_step, args.steps, torch)
-    autograd_ms = autograd_total_ms / args.steps
-    log(f"train step (autograd drop-in) {args.train_points} pts: {autograd_ms:.3f} ms wall/step")
+        def autograd_step():
+            optimizer.zero_grad(set_to_none=True)
+            _, lap_t = fused_laplacian(step_model, x_train)
+            (lap_t - source).pow(2).mean().backward()
+            optimizer.step()
+
+        for _ in range(args.warmup):
+            autograd_step()
+        total_ms, _ = _timed(autograd_step, args.steps, torch)
+        return total_ms / args.steps
+
+    autograd_ms = autograd_timing(True)
+    autograd_unflattened_ms = autograd_timing(False)
+    log(f"train step (autograd drop-in) {args.train_points} pts: {autograd_ms:.3f} ms wall/step "
+        f"(flattened model), {autograd_unflattened_ms:.3f} ms (unflattened)")
 
     # ---- training step (b): the fused step, FusedPoissonAdam (2 kernels) ----
     # All of config 3's outputs: the gradients of every weight and bias and of the input
@@ -404,6 +419,7 @@ def main() -> None:
         "train_step_peak_mib": round(peak_mib, 2),
         "train_step_graphed_ms": round(graph_ms, 5),
         "train_step_autograd_ms": round(autograd_ms, 5),
+        "train_step_autograd_unflattened_ms": round(autograd_unflattened_ms, 5),
         "backward_call_ms": round(bwd_ms, 5),
         "gpu_clock_mhz": clock,
         "roofline": roofline,

@@ -97,6 +97,45 @@ std::vector<torch::Tensor> fused_forward_laplacian_backward(torch::Tensor coordi
   return {grad_parameters, grad_coordinates};
 }
 
+// The backward for the autograd glue (no counterpart among the reference's bindings): either
+// upstream gradient may be None (zero, so no zeros tensor is made), and grad_coordinates is
+// computed only when want_coordinates is set (otherwise None is returned and nothing is
+// written). Same checks and kernels as fused_forward_laplacian_backward.
+std::vector<c10::optional<torch::Tensor>> backward_for_autograd(
+    torch::Tensor coordinates, torch::Tensor parameters, c10::optional<torch::Tensor> grad_output,
+    c10::optional<torch::Tensor> grad_laplacian, bool want_coordinates, int64_t version) {
+  TORCH_CHECK(version >= 1 && version <= 6, "backward version must be 1 to 6");
+  check_inputs(coordinates, parameters);
+  for (const auto* grad : {&grad_output, &grad_laplacian}) {
+    if (!grad->has_value()) continue;
+    const torch::Tensor& g = **grad;
+    TORCH_CHECK(g.is_cuda() && g.is_contiguous() && g.scalar_type() == torch::kFloat32,
+                "upstream gradients must be contiguous float32 CUDA tensors");
+    TORCH_CHECK(g.numel() == coordinates.size(0), "upstream gradients must have [batch] values");
+    TORCH_CHECK(g.device() == coordinates.device(),
+                "upstream gradients must be on the coordinates' device");
+  }
+  const c10::DeviceGuard device_guard(coordinates.device());
+  const int64_t batch = coordinates.size(0);
+  c10::optional<torch::Tensor> grad_coordinates;
+  if (want_coordinates) grad_coordinates = torch::empty_like(coordinates);
+  if (batch == 0) {
+    return {torch::zeros_like(parameters), grad_coordinates};
+  }
+  auto grad_parameters = torch::empty_like(parameters);
+  const size_t workspace_bytes = fhoad_backward_workspace_size(batch);
+  auto workspace = torch::empty({static_cast<int64_t>(workspace_bytes)},
+                                coordinates.options().dtype(torch::kUInt8));
+  check_status(fhoad_forward_laplacian_backward(
+      coordinates.data_ptr<float>(), parameters.data_ptr<float>(),
+      grad_output.has_value() ? grad_output->data_ptr<float>() : nullptr,
+      grad_laplacian.has_value() ? grad_laplacian->data_ptr<float>() : nullptr,
+      grad_parameters.data_ptr<float>(),
+      want_coordinates ? grad_coordinates->data_ptr<float>() : nullptr, workspace.data_ptr(),
+      workspace_bytes, batch, static_cast<int>(version), current_stream(coordinates)));
+  return {grad_parameters, grad_coordinates};
+}
+
 // One fused Poisson PINN + Adam training step (fhoad_poisson_adam_step). No counterpart among
 // the reference's bindings: it replaces the Python step of
 // /root/reference/benchmarks/train_poisson.py:30-45 and benchmark_training.py:41-60 (fused
@@ -167,6 +206,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
              pybind11::arg("grad_coordinates") = pybind11::none(),
              pybind11::arg("boundary") = pybind11::none(),
              pybind11::arg("boundary_weight") = 100.0);
+  module.def("_backward", &backward_for_autograd,
+             "Backward for the autograd glue: optional upstream gradients (None is zero) and an "
+             "optional coordinate gradient",
+             pybind11::arg("coordinates"), pybind11::arg("parameters"),
+             pybind11::arg("grad_output"), pybind11::arg("grad_laplacian"),
+             pybind11::arg("want_coordinates"), pybind11::arg("version") = 6);
   module.def("fused_forward_laplacian", &fused_forward_laplacian,
              "Fixed MLP forward pass and input Laplacian (MI355X HIP kernel)",
              pybind11::arg("coordinates"), pybind11::arg("parameters"),

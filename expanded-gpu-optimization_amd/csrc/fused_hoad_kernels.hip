@@ -1340,8 +1340,8 @@ __device__ __forceinline__ TileInputs load_tile_inputs(const float* __restrict__
     if (kLoss) {
       in.a = seed.source[point];
     } else {
-      in.a = grad_output[point];
-      in.b = grad_laplacian[point];
+      in.a = grad_output ? grad_output[point] : 0.0f;  // a null upstream gradient is zero
+      in.b = grad_laplacian ? grad_laplacian[point] : 0.0f;
     }
   }
   return in;
@@ -1585,7 +1585,7 @@ __device__ __forceinline__ void split_tile(const float* s_w, const float* s_smal
       sc.gx[w][1][m] = gx1;
     }
     __syncthreads();
-    if (w == 0 && g == 0 && active && (!kLoss || (grad_coordinates != nullptr && !on_boundary))) {
+    if (w == 0 && g == 0 && active && grad_coordinates != nullptr && !on_boundary) {
       grad_coordinates[2 * point] = ((sc.gx[0][0][m] + sc.gx[1][0][m]) + sc.gx[2][0][m]) + sc.gx[3][0][m];
       grad_coordinates[2 * point + 1] = ((sc.gx[0][1][m] + sc.gx[1][1][m]) + sc.gx[2][1][m]) + sc.gx[3][1][m];
     }
@@ -1778,7 +1778,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         acc.b0 += row_reduce_scatter16(tb, m_pick);
         gx0 = sum_lane_groups(gx0);
         gx1 = sum_lane_groups(gx1);
-        if (g == 0 && active && (!kLoss || grad_coordinates != nullptr)) {
+        if (g == 0 && active && grad_coordinates != nullptr) {
           grad_coordinates[2 * point] = gx0;
           grad_coordinates[2 * point + 1] = gx1;
         }
@@ -1959,8 +1959,8 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
         if (kLoss) {
           if (!on_boundary) f = seed.source[point];
         } else {
-          gu = grad_output[point];
-          gl = grad_laplacian[point];
+          gu = grad_output ? grad_output[point] : 0.0f;  // a null upstream gradient is zero
+          gl = grad_laplacian ? grad_laplacian[point] : 0.0f;
         }
       }
 
@@ -2386,9 +2386,7 @@ extern "C" int fhoad_forward_laplacian_backward(const float* coordinates, const 
                        grad_parameters, static_cast<int64_t>(kParameterCount));
     return check_launch("fill_zero_kernel");
   }
-  if (!coordinates || !grad_output || !grad_laplacian || !grad_coordinates) {
-    return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
-  }
+  if (!coordinates) return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
   const size_t needed = fhoad_backward_workspace_size(batch);
   if (!workspace || workspace_bytes < needed) {
     return fail(FHOAD_ERROR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes,
@@ -2414,9 +2412,7 @@ extern "C" int fhoad_forward_laplacian_backward_noalloc(
                        grad_parameters, static_cast<int64_t>(kParameterCount));
     return check_launch("fill_zero_kernel");
   }
-  if (!coordinates || !grad_output || !grad_laplacian || !grad_coordinates) {
-    return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
-  }
+  if (!coordinates) return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
   const size_t needed = fhoad_backward_workspace_size(batch);
   if (needed > kNoAllocScratchBytes) {
     return fail(FHOAD_ERROR_WORKSPACE, "batch %lld needs %zu bytes of scratch, the static scratch holds %zu",

@@ -13,10 +13,15 @@ import weakref
 import torch
 from torch import Tensor, nn
 
-from fused_hoad._extension import fused_forward_laplacian, fused_forward_laplacian_backward
+from fused_hoad._extension import (
+    fused_forward_laplacian,
+    fused_forward_laplacian_backward,
+    load_extension,
+)
 from fused_hoad.backends.forward_laplacian import tanh_mlp_forward_laplacian
 from fused_hoad.parameters import (
     POISSON_PARAMETER_LAYOUT,
+    _linear_layers,
     flattened_poisson_parameters,
     pack_poisson_parameters,
     unpack_poisson_parameters,
@@ -65,6 +70,70 @@ class FusedForwardLaplacian(torch.autograd.Function):
             coordinates, parameters, grad_output, grad_laplacian, needs_coordinates, needs_parameters
         )
         return grad_coordinates, grad_parameters, None, None
+
+
+class FlattenedFusedLaplacian(torch.autograd.Function):
+    """``FusedForwardLaplacian`` for a model whose parameters are views of one packed buffer
+    (``flatten_poisson_parameters_``): the kernels read that buffer directly, the autograd
+    inputs are the model's ten parameters themselves, and the backward hands each one a view
+    of the packed gradient. A training step then has no ``torch.cat`` pack, no cat backward
+    and no per-parameter gradient copies. An output the loss does not use reaches the
+    backward as ``None``, which the kernel reads as zero (no zeros tensor is made), and the
+    coordinate gradient is computed only when the coordinates require it."""
+
+    @staticmethod
+    def forward(ctx, coordinates: Tensor, flat: Tensor, version: int, backward: str, *parameters: Tensor):
+        ctx.save_for_backward(coordinates, flat)
+        ctx.backward_mode = backward
+        ctx.set_materialize_grads(False)
+        return fused_forward_laplacian(coordinates, flat, version)
+
+    @staticmethod
+    def backward(ctx, grad_output: Tensor | None, grad_laplacian: Tensor | None):
+        coordinates, flat = ctx.saved_tensors
+        needs_coordinates = ctx.needs_input_grad[0]
+        needs_parameters = any(ctx.needs_input_grad[4:])
+        if grad_output is None and grad_laplacian is None:
+            return (None,) * (4 + len(POISSON_PARAMETER_LAYOUT) * 2)
+        mode = ctx.backward_mode
+        if mode in _CUDA_BACKWARD_VERSIONS:
+            grad_flat, grad_coordinates = load_extension()._backward(
+                coordinates,
+                flat,
+                None if grad_output is None else grad_output.reshape(-1).contiguous(),
+                None if grad_laplacian is None else grad_laplacian.reshape(-1).contiguous(),
+                needs_coordinates,
+                _CUDA_BACKWARD_VERSIONS[mode],
+            )
+        else:
+            zeros = torch.zeros(coordinates.shape[0], 1, dtype=flat.dtype, device=flat.device)
+            grad_coordinates, grad_flat = _recompute_backward(
+                coordinates,
+                flat,
+                zeros if grad_output is None else grad_output,
+                zeros if grad_laplacian is None else grad_laplacian,
+                needs_coordinates,
+                True,
+            )
+        grads: list[Tensor | None] = []
+        for spec, needs in zip(POISSON_PARAMETER_LAYOUT, _pairs(ctx.needs_input_grad[4:]), strict=True):
+            grads.append(
+                grad_flat[spec.weight_offset : spec.bias_offset].view(spec.out_features, spec.in_features)
+                if needs[0] else None
+            )
+            grads.append(grad_flat[spec.bias_offset : spec.end_offset] if needs[1] else None)
+        if not needs_parameters:
+            grads = [None] * len(grads)
+        return (grad_coordinates if needs_coordinates else None, None, None, None, *grads)
+
+
+def _pairs(flags):
+    return [(flags[i], flags[i + 1]) for i in range(0, len(flags), 2)]
+
+
+def _flattened_parameter_list(model: nn.Module) -> list[Tensor]:
+    """The model's weights and biases in packed-layout order."""
+    return [t for layer in _linear_layers(model) for t in (layer.weight, layer.bias)]
 
 
 def _recompute_backward(
@@ -127,6 +196,13 @@ def fused_laplacian(
     """
     if backward not in BACKWARD_MODES:
         raise ValueError(f"backward must be one of {BACKWARD_MODES}")
+    if torch.is_grad_enabled():
+        flat = flattened_poisson_parameters(model)
+        if flat is not None:  # parameters are views of the packed buffer: no pack at all
+            tensors = _flattened_parameter_list(model)
+            if coordinates.requires_grad or any(t.requires_grad for t in tensors):
+                return FlattenedFusedLaplacian.apply(coordinates.contiguous(), flat, version, backward, *tensors)
+            return fused_forward_laplacian(coordinates.contiguous(), flat, version)
     parameters = _packed_parameters(model)
     if parameters.requires_grad or coordinates.requires_grad:
         return FusedForwardLaplacian.apply(coordinates.contiguous(), parameters, version, backward)

@@ -73,7 +73,9 @@ size_t fhoad_backward_workspace_size(int64_t batch);
  * Backward of the forward Laplacian. Given dLoss/du (grad_output[batch]) and
  * dLoss/dLaplacian (grad_laplacian[batch]), writes dLoss/dparameters (grad_parameters[12737],
  * overwritten, not accumulated) and dLoss/dcoordinates (grad_coordinates[batch][2]).
- * workspace must hold
+ * grad_output or grad_laplacian may be NULL, meaning all zeros (a loss that uses only u or
+ * only the Laplacian), and grad_coordinates may be NULL, meaning not written; the reference
+ * requires all three. workspace must hold
  * fhoad_backward_workspace_size(batch) bytes and be 16-byte aligned (hipMalloc and torch
  * allocations are); its contents on entry are ignored. The
  * weight-gradient sum runs in a fixed order that does not depend on the grid size, so

@@ -191,6 +191,18 @@ def test_raw_entry_points_match_the_torch_extension() -> None:
     ep, ex = _C.fused_forward_laplacian_backward(x, p, gu, gl)
     torch.cuda.synchronize()
     assert torch.equal(gp, ep) and torch.equal(gx, ex)
+    # null upstream gradients read as zeros, a null grad_coordinates is not written
+    zeros = torch.zeros_like(gu)
+    for null_u, null_l in ((True, False), (False, True)):
+        gp_null = torch.empty(12737, device="cuda")
+        status = lib.fhoad_forward_laplacian_backward(
+            x.data_ptr(), p.data_ptr(), None if null_u else gu.data_ptr(),
+            None if null_l else gl.data_ptr(), gp_null.data_ptr(), None, ws.data_ptr(), ws_bytes,
+            batch, 6, stream)
+        assert status == 0, lib.fhoad_last_error()
+        ep0, _ = _C.fused_forward_laplacian_backward(x, p, zeros if null_u else gu, zeros if null_l else gl)
+        torch.cuda.synchronize()
+        assert torch.equal(gp_null, ep0), (null_u, null_l)
     # a workspace one byte short is refused
     status = lib.fhoad_forward_laplacian_backward(
         x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), gp.data_ptr(), gx.data_ptr(),

@@ -54,6 +54,52 @@ def test_fused_gradients_match_forward_laplacian(name: str) -> None:
         torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-4)
 
 
+@pytest.mark.parametrize(
+    "loss_kind,coordinate_grad,mode",
+    [("lap", False, "cuda"), ("lap", True, "cuda"), ("u_and_lap", True, "cuda"),
+     ("u", False, "cuda"), ("lap", True, "recompute")],
+)
+def test_flattened_model_gradients_equal_the_packed_path(loss_kind: str, coordinate_grad: bool,
+                                                         mode: str) -> None:
+    """A model flattened with flatten_poisson_parameters_ takes the no-pack autograd path
+    (its parameters are the Function's inputs, their gradients views of the packed one, an
+    unused output's gradient is read as zero without a zeros tensor, the coordinate gradient is
+    skipped unless needed). Its gradients are bitwise those of the torch.cat path of an
+    unflattened twin, which passes materialized zeros and always computes grad_coordinates."""
+    announce(f"flattened vs packed autograd path, loss={loss_kind}, coordinate grad={coordinate_grad}, backward={mode}")
+    from fused_hoad import manufactured_source
+    from fused_hoad.backends.fused import fused_laplacian
+    from fused_hoad.parameters import flatten_poisson_parameters_, flattened_poisson_parameters
+
+    x0 = coordinates(5000, seed=31)
+    f = manufactured_source(x0)
+
+    def run(model):
+        model.zero_grad(set_to_none=True)
+        x = x0.clone().requires_grad_(coordinate_grad)
+        u, lap = fused_laplacian(model, x, backward=mode)
+        terms = {"lap": (lap - f).pow(2).mean(), "u": u.pow(2).mean()}
+        loss = terms["lap"] + terms["u"] if loss_kind == "u_and_lap" else terms[loss_kind]
+        loss.backward()
+        grads = [p.grad for p in model.parameters()]
+        return grads, (x.grad if coordinate_grad else None)
+
+    packed_model = _model(4)
+    flat_model = _model(4)
+    flatten_poisson_parameters_(flat_model)
+    assert flattened_poisson_parameters(flat_model) is not None
+    want, want_x = run(packed_model)
+    got, got_x = run(flat_model)
+    torch.cuda.synchronize()
+    for index, (a, b) in enumerate(zip(got, want, strict=True)):
+        if b is None:  # a parameter the loss does not reach (b_out for a Laplacian-only loss)
+            assert a is None or torch.count_nonzero(a).item() == 0, index
+            continue
+        assert torch.equal(a, b), f"parameter {index}"
+    if coordinate_grad:
+        assert torch.equal(got_x, want_x)
+
+
 def test_fused_trains_like_forward_laplacian() -> None:
     announce("50 Adam steps, fused vs forward_laplacian, batch=2048")
     from fused_hoad import forward_laplacian, get_backend
