@@ -91,6 +91,31 @@ constexpr int kSmallFloats = kSmallBout + 4;
 __device__ __forceinline__ int lane_rows(int m, int g) { return kWRow * m + 4 * g; }
 __device__ __forceinline__ int lane_cols(int m, int g) { return 272 * g + m; }
 
+// The backward's dW staging planes hold [neuron row R][tile point p] at pitch 80, with the
+// point index XOR-ed with 24 in rows whose bit 2 is set:
+//   (R, p) at 80 R + (p ^ (24 ((R >> 2) & 1))).
+// They are written 4 bytes per lane (lane (m, g): rows 4 g + r of a 16-row block, point m of
+// a 16-point block) and read 16 bytes per lane (row m, points 4 g .. 4 g + 3 of a block).
+// Measured on gfx950 with probe kernels that issue exactly these two patterns
+// (SQ_LDS_BANK_CONFLICT): at pitch 68 without the XOR, as the weight planes are, every 16-byte
+// read costs 4 conflict cycles and the writes none; with this layout neither conflicts. (At
+// pitch 72 with the 16-point blocks swapped on row bit 3 both patterns conflicted.)
+constexpr int kSRow = 80;
+constexpr int kSPlane = 64 * kSRow;
+// Write base of lane (m, g) in wave w: row 4 g (+ 16 mb + r, immediates), point 16 w + m.
+// (4 g + r) >> 2 = g, so the XOR is a lane constant.
+__device__ __forceinline__ int stage_lane_cols(int m, int g, int w) {
+  return 4 * kSRow * g + ((16 * w + m) ^ (24 * (g & 1)));
+}
+// Read base of lane (m, g) for point block ns of row 16 b + m: with t = (m >> 2) & 1 the
+// points 16 ns + 4 g .. + 3 sit at 16 (ns ^ t) + 4 (g ^ 2 t), so even blocks are 16 t floats
+// further and odd blocks 16 t floats nearer than 16 ns. `odd` selects the base for odd ns; ns
+// itself stays an immediate.
+__device__ __forceinline__ int stage_lane_rows(int m, int g, bool odd) {
+  const int t = (m >> 2) & 1;
+  return kSRow * m + 4 * (g ^ (2 * t)) + (odd ? -16 * t : 16 * t);
+}
+
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -412,12 +437,16 @@ __device__ __forceinline__ T opaque(T x) {
 // them as per-tile LDS reads.
 __device__ __forceinline__ void keep_lds_reads_in_loop() { __asm__ volatile("" ::: "memory"); }
 
-// A scheduling fence that LDS accesses and MFMAs do not cross; VALU and SALU instructions may.
-// Placed between the LDS reads for the next step and the MFMAs of the current one, it keeps
-// the reads issued a step ahead (at full register use the scheduler otherwise sinks each read
-// to just before its first use, and the MFMA then waits out the LDS latency), while the
-// VALU work around them can still fill MFMA latencies.
-__device__ __forceinline__ void lds_mfma_fence() { __builtin_amdgcn_sched_barrier(0x0406); }
+// A scheduling fence that only SALU instructions cross. Placed between the LDS reads for the
+// next step and the MFMAs of the current one, it keeps the reads issued a step ahead (at full
+// register use the scheduler otherwise sinks each read to just before its first use, and the
+// MFMA then waits out the LDS latency). It also keeps VALU work out of the MFMA runs: FP32
+// MFMA and VALU never execute together on gfx950, and a VALU instruction issued right after an
+// MFMA costs about 8 cycles more than one issued after another VALU instruction (measured with
+// a one-wave probe: 1 MFMA + k independent FMAs take 32.5 + 8 + 4.7 k cycles, 4 MFMAs + 16
+// FMAs no more than their separate times). Letting VALU cross, the scheduler had spread single
+// instructions between MFMAs, about 250 such switches per backward tile; with this fence 57.
+__device__ __forceinline__ void lds_mfma_fence() { __builtin_amdgcn_sched_barrier(0x0004); }
 
 // Value of lane l ^ 32 (permlane32) or l ^ 16 (permlane16) in every lane, with gfx950's
 // v_permlane32_swap / v_permlane16_swap (VALU, no LDS round trip). swap(u, 0) leaves the
@@ -831,30 +860,31 @@ static_assert(kMaxSlots % kReduceGroups == 0, "reduction tree must tile the slot
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
 // Stage two jet components of this wave's zbar and h_prev into the dW staging buffer: planes
-// of [neuron][tile point] at pitch 68, so this lane's value of neuron 16 mb + 4 g + r at point
-// 16 w + m lands at stage_lane + 1088 mb + 68 r. zbar components go to planes 0, 1 and h_prev
-// components to planes 2, 3.
+// of [neuron][tile point] (kSRow layout), so this lane's value of neuron 16 mb + 4 g + r at
+// point 16 w + m lands at stage_lane + 16 kSRow mb + kSRow r (stage_lane_cols holds the swap).
+// zbar components go to planes 0, 1 and h_prev components to planes 2, 3.
 __device__ __forceinline__ void stage_write(float* stage_lane, int mb, int r, float z_a,
                                             float z_b, float h_a, float h_b) {
-  float* p = stage_lane + 1088 * mb + kWRow * r;
+  float* p = stage_lane + 16 * kSRow * mb + kSRow * r;
   p[0] = z_a;
-  p[kPlane] = z_b;
-  p[2 * kPlane] = h_a;
-  p[3 * kPlane] = h_b;
+  p[kSPlane] = z_b;
+  p[2 * kSPlane] = h_a;
+  p[3 * kSPlane] = h_b;
 }
 
 // dW[16 w + ., 16 nb + .] += sum over (2 staged components, 64 points) of zbar h_prev^T.
 // Lane (m, g) reads zbar[16 w + m][p] and h_prev[16 nb + m][p] for p = 16 s + 4 g + k,
-// k = 0..3, as 16-byte reads (stage_rows = this lane's 68 m + 4 g), so the MFMA contracts over
-// points. Returns the sum of this lane's plane-0 zbar reads (the bias gradient partial when
-// plane 0 holds zbar_v).
-__device__ __forceinline__ float dw_product(const float* stage_rows, int w, f4 (&dw)[4]) {
+// k = 0..3, as 16-byte reads (rows_even / rows_odd: stage_lane_rows for even / odd s), so the
+// MFMA contracts over points; every lane supplies the same points at each step. Returns the
+// sum of this lane's plane-0 zbar reads (the bias gradient partial when plane 0 holds zbar_v).
+__device__ __forceinline__ float dw_product(const float* rows_even, const float* rows_odd, int w,
+                                            f4 (&dw)[4]) {
   float bias = 0.0f;
   // Steps (cc, s) in order; each step's five 16-byte operands are read one step ahead.
   f4 na, nb[4];
-  na = lds4(stage_rows + 1088 * w);
+  na = lds4(rows_even + 16 * kSRow * w);
 #pragma unroll
-  for (int b = 0; b < 4; ++b) nb[b] = lds4(stage_rows + 2 * kPlane + 1088 * b);
+  for (int b = 0; b < 4; ++b) nb[b] = lds4(rows_even + 2 * kSPlane + 16 * kSRow * b);
 #pragma unroll
   for (int step = 0; step < 8; ++step) {
     const int cc = step >> 2;
@@ -864,9 +894,10 @@ __device__ __forceinline__ float dw_product(const float* stage_rows, int w, f4 (
     for (int k = 0; k < 4; ++k) b[k] = nb[k];
     if (step < 7) {
       const int ncc = (step + 1) >> 2, ns = (step + 1) & 3;
-      na = lds4(stage_rows + ncc * kPlane + 1088 * w + 16 * ns);
+      const float* rows = (ns & 1) ? rows_odd : rows_even;
+      na = lds4(rows + ncc * kSPlane + 16 * kSRow * w + 16 * ns);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) nb[k] = lds4(stage_rows + (2 + ncc) * kPlane + 1088 * k + 16 * ns);
+      for (int k = 0; k < 4; ++k) nb[k] = lds4(rows + (2 + ncc) * kSPlane + 16 * kSRow * k + 16 * ns);
     }
     lds_mfma_fence();
 #pragma unroll
@@ -893,7 +924,8 @@ __device__ __forceinline__ int owned_neuron(int m, int g) { return 16 * (m >> 2)
 // layer 0's own adjoint. Adds the bias gradient sum_p zbar_v' = sum_p zbar_v / c to g_bias.
 __device__ __forceinline__ void stage_and_dw_layer0(const f4 (&zbar)[4][4], f4 (&dw)[4],
                                                     float& g_bias, float* stage_lane,
-                                                    const float* stage_rows, const float* s_small,
+                                                    const float* rows_even, const float* rows_odd,
+                                                    const float* s_small,
                                                     int w, int g, float x0, float x1,
                                                     f4 (&pv)[4], f4 (&ps)[4]) {
   __syncthreads();  // previous readers of the staging buffer are done
@@ -911,7 +943,7 @@ __device__ __forceinline__ void stage_and_dw_layer0(const f4 (&zbar)[4][4], f4 (
     }
   }
   __syncthreads();
-  g_bias += sum_lane_groups(dw_product(stage_rows, w, dw));
+  g_bias += sum_lane_groups(dw_product(rows_even, rows_odd, w, dw));
   __syncthreads();
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
@@ -923,7 +955,7 @@ __device__ __forceinline__ void stage_and_dw_layer0(const f4 (&zbar)[4][4], f4 (
     }
   }
   __syncthreads();
-  dw_product(stage_rows, w, dw);
+  dw_product(rows_even, rows_odd, w, dw);
 }
 
 // ---- the interior tiles of backward_kernel: the walk back from each layer's tanh-jet output ----
@@ -1075,7 +1107,8 @@ __device__ __forceinline__ void adjoint_through(const float* w, const f4 (&zb)[4
 // sum_p zbar_v' to g_bias.
 __device__ __forceinline__ void stage_and_dw_h(const f4 (&zbar)[4][4], const f4 (&hp)[4][4],
                                                f4 (&dw)[4], float& g_bias, float* stage_lane,
-                                               const float* stage_rows, int w) {
+                                               const float* rows_even, const float* rows_odd,
+                                               int w) {
   __syncthreads();  // previous readers of the staging buffer are done
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
@@ -1085,7 +1118,7 @@ __device__ __forceinline__ void stage_and_dw_h(const f4 (&zbar)[4][4], const f4 
     }
   }
   __syncthreads();
-  g_bias += sum_lane_groups(dw_product(stage_rows, w, dw));
+  g_bias += sum_lane_groups(dw_product(rows_even, rows_odd, w, dw));
   __syncthreads();
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
@@ -1095,7 +1128,7 @@ __device__ __forceinline__ void stage_and_dw_h(const f4 (&zbar)[4][4], const f4 
     }
   }
   __syncthreads();
-  dw_product(stage_rows, w, dw);
+  dw_product(rows_even, rows_odd, w, dw);
 }
 
 // Seed of the fused Poisson training step (kLoss). The loss is the PINN loss
@@ -1152,7 +1185,7 @@ constexpr int kBndPitch = 20;                                   // transposed ro
 constexpr int kBndExchange = 0;                                 // [2][4 waves][64 lanes] f4
 constexpr int kBndH = kBndExchange + 2 * kBwdWaves * kWave * 4;  // [3 layers][64 rows][pitch]
 constexpr int kBndZ = kBndH + 3 * kHidden * kBndPitch;          // [2][4 waves][16 rows][pitch]
-static_assert(kBndZ + 2 * kBwdWaves * 16 * kBndPitch <= 4 * kPlane,
+static_assert(kBndZ + 2 * kBwdWaves * 16 * kBndPitch <= 4 * kSPlane,
               "the boundary tile's scratch must fit the dW staging buffer");
 
 // Store this lane's 4 rows row0 + 4 g + r (value at point m) into a transposed buffer.
@@ -1605,7 +1638,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
                 float* __restrict__ grad_coordinates, float* __restrict__ partials,
                 int64_t batch, int64_t whole, int64_t tiles, int slots, LossSeed seed) {
   constexpr int kStageFloats =
-      kRest && kSplitScratchFloats > 4 * kPlane ? kSplitScratchFloats : 4 * kPlane;
+      kRest && kSplitScratchFloats > 4 * kSPlane ? kSplitScratchFloats : 4 * kSPlane;
   __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ __attribute__((aligned(16))) float s_stage[kStageFloats];
@@ -1628,7 +1661,9 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   // span more than the 64 KB reach of a DS offset, and hoisted bases would be spilled.
   const int rows_off = lane_rows(m, g);
   const int cols_off = lane_cols(m, g);
-  const int stage_lane_off = cols_off + 16 * w;
+  const int stage_lane_off = stage_lane_cols(m, g, w);
+  const int stage_even_off = stage_lane_rows(m, g, false);
+  const int stage_odd_off = stage_lane_rows(m, g, true);
 
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
     WaveSums acc;
@@ -1726,19 +1761,20 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 
       // ---- 3. hidden layer 3: dW3 from (zbar3, h2), then W3^T zbar3 into layer 2's adjoint ----
       stage_and_dw_h(h3, h2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
-                     s_stage + opaque(rows_off), w);
+                     s_stage + opaque(stage_even_off), s_stage + opaque(stage_odd_off), w);
       adjoint_through(s_w + opaque(cols_off) + 2 * kPlane, h3, h2);
 
       // ---- 4. hidden layer 2: dW2 from (zbar2, h1), then W2^T zbar2 into layer 1's adjoint ----
       stage_and_dw_h(h2, h1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
-                     s_stage + opaque(rows_off), w);
+                     s_stage + opaque(stage_even_off), s_stage + opaque(stage_odd_off), w);
       deliver(next);  // the next tile's inputs, before this tile's stores
       adjoint_through(s_w + opaque(cols_off) + kPlane, h2, h1);
 
       // ---- 5. hidden layer 1: dW1 from (zbar1, h0), h0 rebuilt with its (v', s') ----
       f4 v0[4], s0[4];
       stage_and_dw_layer0(h1, acc.dw[0], acc.bh[0], s_stage + opaque(stage_lane_off),
-                          s_stage + opaque(rows_off), s_small, w, g, x0, x1, v0, s0);
+                          s_stage + opaque(stage_even_off), s_stage + opaque(stage_odd_off),
+                          s_small, w, g, x0, x1, v0, s0);
 
       // ---- 6. W1^T zbar1, one block at a time, into layer 0 in closed form ----
       // bv is the adjoint of z'_v = c z_v and bj_d that of z'_Jd = 2 W0[:, d], so
