@@ -11,8 +11,9 @@ update), ``train_step_graphed_ms`` the same replayed from a HIP graph, and
 ``train_step_autograd_ms`` the reference's step through the drop-in API (fused forward +
 autograd loss + fused backward + torch.optim.Adam) on a model flattened once with
 ``flatten_poisson_parameters_`` (``train_step_autograd_unflattened_ms``: on the model as
-built). ``train_step_no_coordinate_grad_ms`` is the fused step without the coordinate
-gradient, a labelled variant only.
+built), ``train_step_autograd_graphed_ms`` that drop-in step captured whole in a HIP graph
+(the reference's "whole step CUDA-graph captured" row). ``train_step_no_coordinate_grad_ms`` is
+the fused step without the coordinate gradient, a labelled variant only.
 
 ``roofline.traffic`` comes from the committed rocprofv3 summary
 profiles/forward_kernel_65536_traffic.json only when that was measured on the kernel source
@@ -188,7 +189,7 @@ def main() -> None:
     )
     from fused_hoad.backends.fused import _recompute_backward, fused_laplacian
     from fused_hoad.parameters import flatten_poisson_parameters_, pack_poisson_parameters
-    from fused_hoad.training import FusedPoissonAdam
+    from fused_hoad.training import FusedPoissonAdam, cuda_graph_step
 
     load_extension()  # fail loudly if the HIP extension is missing
     if not torch.cuda.is_available():
@@ -282,6 +283,54 @@ def main() -> None:
     autograd_unflattened_ms = autograd_timing(False)
     log(f"train step (autograd drop-in) {args.train_points} pts: {autograd_ms:.3f} ms wall/step "
         f"(flattened model), {autograd_unflattened_ms:.3f} ms (unflattened)")
+
+    # The same drop-in step captured whole in a HIP graph (cuda_graph_step: forward, autograd
+    # loss and backward, Adam with capturable=True), the form of the reference's "whole step
+    # CUDA-graph captured" row. Before timing, every replay of a short run is checked against
+    # the same steps run eagerly from the same weights (the loss each step, rtol 1e-4, and the
+    # weights after); a graph that replays wrongly is not timed (the field is null and
+    # train_step_autograd_graphed_note says why).
+    def autograd_graph_timing():
+        def make():
+            torch.manual_seed(0)
+            model = build_mlp(DEFAULT_POISSON_MLP).to(device)
+            flatten_poisson_parameters_(model)
+            return model
+
+        def loss_of(model):
+            def loss_fn():
+                _, lap_t = fused_laplacian(model, x_train)
+                return (lap_t - source).pow(2).mean()
+            return loss_fn
+
+        graph_model, eager_model = make(), make()
+        graph_opt = torch.optim.Adam(graph_model.parameters(), lr=1e-3, capturable=True)
+        eager_opt = torch.optim.Adam(eager_model.parameters(), lr=1e-3)
+        replay = cuda_graph_step(loss_of(graph_model), graph_opt, warmup=3)
+        eager_loss = loss_of(eager_model)
+        for k in range(3 + 10):
+            eager_opt.zero_grad(set_to_none=True)
+            loss = eager_loss()
+            loss.backward()
+            eager_opt.step()
+            if k >= 3:
+                got, want = replay().item(), loss.item()
+                if abs(got - want) > 1e-4 * abs(want):
+                    return None, f"replay {k - 3} loss {got} differs from the eager step's {want}"
+        for a, b in zip(graph_model.parameters(), eager_model.parameters()):
+            if not torch.allclose(a, b, rtol=1e-4, atol=1e-6):
+                return None, "weights after 10 replays differ from those after 10 eager steps"
+        for _ in range(args.warmup):
+            replay()
+        total_ms, _ = _timed(replay, args.steps, torch)
+        return total_ms / args.steps, "10 replays checked against eager steps (loss rtol 1e-4, weights)"
+
+    autograd_graph_ms, autograd_graph_note = autograd_graph_timing()
+    if autograd_graph_ms is None:
+        log(f"train step (autograd drop-in, whole step in a HIP graph): not timed, {autograd_graph_note}")
+    else:
+        log(f"train step (autograd drop-in, whole step in a HIP graph) {args.train_points} pts: "
+            f"{autograd_graph_ms:.3f} ms wall/step (flattened model; {autograd_graph_note})")
 
     # ---- training step (b): the fused step, FusedPoissonAdam (2 kernels) ----
     # All of config 3's outputs: the gradients of every weight and bias and of the input
@@ -420,6 +469,8 @@ def main() -> None:
         "train_step_graphed_ms": round(graph_ms, 5),
         "train_step_autograd_ms": round(autograd_ms, 5),
         "train_step_autograd_unflattened_ms": round(autograd_unflattened_ms, 5),
+        "train_step_autograd_graphed_ms": None if autograd_graph_ms is None else round(autograd_graph_ms, 5),
+        "train_step_autograd_graphed_note": autograd_graph_note,
         "backward_call_ms": round(bwd_ms, 5),
         "gpu_clock_mhz": clock,
         "roofline": roofline,

@@ -164,6 +164,50 @@ def test_graph_captured_training_step_matches_eager_step() -> None:
     torch.testing.assert_close(torch.tensor(train(True)), torch.tensor(train(False)), rtol=1e-4, atol=0)
 
 
+def test_graph_captured_flattened_step_matches_eager_at_64k() -> None:
+    """The drop-in step bench.py times as train_step_autograd_graphed_ms: a flattened model at
+    65,536 points (BASELINE config 3's size, where torch's mean reduces over many blocks),
+    captured whole and replayed 10 times with a host sync between replays, against the same
+    steps run eagerly: every replay's loss (rtol 1e-4) and the weights after."""
+    announce("whole-step graph capture vs eager, flattened model, batch=65536")
+    from fused_hoad import manufactured_source
+    from fused_hoad.backends.fused import fused_laplacian
+    from fused_hoad.parameters import flatten_poisson_parameters_
+    from fused_hoad.training import cuda_graph_step
+
+    x = coordinates(65536, seed=8)
+    f = manufactured_source(x)
+
+    def make():
+        model = _model(5)
+        flatten_poisson_parameters_(model)
+        return model
+
+    def loss_of(model):
+        def loss_fn():
+            _, lap = fused_laplacian(model, x)
+            return (lap - f).pow(2).mean()
+        return loss_fn
+
+    graph_model, eager_model = make(), make()
+    graph_opt = torch.optim.Adam(graph_model.parameters(), lr=1e-3, capturable=True)
+    eager_opt = torch.optim.Adam(eager_model.parameters(), lr=1e-3)
+    replay = cuda_graph_step(loss_of(graph_model), graph_opt, warmup=3)
+    eager_loss = loss_of(eager_model)
+    got, want = [], []
+    for k in range(13):
+        eager_opt.zero_grad(set_to_none=True)
+        loss = eager_loss()
+        loss.backward()
+        eager_opt.step()
+        if k >= 3:
+            got.append(replay().item())
+            want.append(loss.item())
+    torch.testing.assert_close(torch.tensor(got), torch.tensor(want), rtol=1e-4, atol=0)
+    for a, b in zip(graph_model.parameters(), eager_model.parameters(), strict=True):
+        torch.testing.assert_close(a, b, rtol=1e-4, atol=1e-6)
+
+
 def _poisson_step_losses(batch: int, steps: int, backward: str):
     from fused_hoad import manufactured_source
     from fused_hoad.backends.fused import fused_laplacian
