@@ -12,8 +12,10 @@ update), ``train_step_graphed_ms`` the same replayed from a HIP graph, and
 autograd loss + fused backward + torch.optim.Adam) on a model flattened once with
 ``flatten_poisson_parameters_`` (``train_step_autograd_unflattened_ms``: on the model as
 built), ``train_step_autograd_graphed_ms`` that drop-in step captured whole in a HIP graph
-(the reference's "whole step CUDA-graph captured" row). ``train_step_no_coordinate_grad_ms`` is
-the fused step without the coordinate gradient, a labelled variant only.
+(the reference's "whole step CUDA-graph captured" row), and
+``train_step_autograd_graphed_fused_adam_ms`` the same with ``torch.optim.Adam(fused=True)``.
+``train_step_no_coordinate_grad_ms`` is the fused step without the coordinate gradient, a
+labelled variant only.
 
 ``roofline.traffic`` comes from the committed rocprofv3 summary
 profiles/forward_kernel_65536_traffic.json only when that was measured on the kernel source
@@ -290,7 +292,7 @@ def main() -> None:
     # the same steps run eagerly from the same weights (the loss each step, rtol 1e-4, and the
     # weights after); a graph that replays wrongly is not timed (the field is null and
     # train_step_autograd_graphed_note says why).
-    def autograd_graph_timing():
+    def autograd_graph_timing(fused_adam: bool):
         def make():
             torch.manual_seed(0)
             model = build_mlp(DEFAULT_POISSON_MLP).to(device)
@@ -304,8 +306,12 @@ def main() -> None:
             return loss_fn
 
         graph_model, eager_model = make(), make()
-        graph_opt = torch.optim.Adam(graph_model.parameters(), lr=1e-3, capturable=True)
-        eager_opt = torch.optim.Adam(eager_model.parameters(), lr=1e-3)
+        if fused_adam:
+            graph_opt = torch.optim.Adam(graph_model.parameters(), lr=1e-3, fused=True, capturable=True)
+            eager_opt = torch.optim.Adam(eager_model.parameters(), lr=1e-3, fused=True)
+        else:
+            graph_opt = torch.optim.Adam(graph_model.parameters(), lr=1e-3, capturable=True)
+            eager_opt = torch.optim.Adam(eager_model.parameters(), lr=1e-3)
         replay = cuda_graph_step(loss_of(graph_model), graph_opt, warmup=3)
         eager_loss = loss_of(eager_model)
         for k in range(3 + 10):
@@ -325,12 +331,22 @@ def main() -> None:
         total_ms, _ = _timed(replay, args.steps, torch)
         return total_ms / args.steps, "10 replays checked against eager steps (loss rtol 1e-4, weights)"
 
-    autograd_graph_ms, autograd_graph_note = autograd_graph_timing()
-    if autograd_graph_ms is None:
-        log(f"train step (autograd drop-in, whole step in a HIP graph): not timed, {autograd_graph_note}")
-    else:
-        log(f"train step (autograd drop-in, whole step in a HIP graph) {args.train_points} pts: "
-            f"{autograd_graph_ms:.3f} ms wall/step (flattened model; {autograd_graph_note})")
+    def checked_graph_timing(fused_adam: bool):
+        try:
+            return autograd_graph_timing(fused_adam)
+        except RuntimeError as err:  # a capture this torch build refuses: reported, not fatal
+            return None, f"capture failed: {err}"
+
+    autograd_graph_ms, autograd_graph_note = checked_graph_timing(False)
+    # labelled variant: the same with torch.optim.Adam(fused=True) (one optimizer kernel)
+    autograd_graph_fused_ms, autograd_graph_fused_note = checked_graph_timing(True)
+    for label, ms, note in (("foreach Adam", autograd_graph_ms, autograd_graph_note),
+                            ("Adam(fused=True)", autograd_graph_fused_ms, autograd_graph_fused_note)):
+        if ms is None:
+            log(f"train step (autograd drop-in, whole step in a HIP graph, {label}): not timed, {note}")
+        else:
+            log(f"train step (autograd drop-in, whole step in a HIP graph, {label}) {args.train_points} pts: "
+                f"{ms:.3f} ms wall/step (flattened model; {note})")
 
     # ---- training step (b): the fused step, FusedPoissonAdam (2 kernels) ----
     # All of config 3's outputs: the gradients of every weight and bias and of the input
@@ -471,6 +487,8 @@ def main() -> None:
         "train_step_autograd_unflattened_ms": round(autograd_unflattened_ms, 5),
         "train_step_autograd_graphed_ms": None if autograd_graph_ms is None else round(autograd_graph_ms, 5),
         "train_step_autograd_graphed_note": autograd_graph_note,
+        "train_step_autograd_graphed_fused_adam_ms": (None if autograd_graph_fused_ms is None
+                                                      else round(autograd_graph_fused_ms, 5)),
         "backward_call_ms": round(bwd_ms, 5),
         "gpu_clock_mhz": clock,
         "roofline": roofline,
