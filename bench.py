@@ -13,7 +13,10 @@ autograd loss + fused backward + torch.optim.Adam) on a model flattened once wit
 ``flatten_poisson_parameters_`` (``train_step_autograd_unflattened_ms``: on the model as
 built), ``train_step_autograd_graphed_ms`` that drop-in step captured whole in a HIP graph
 (the reference's "whole step CUDA-graph captured" row), and
-``train_step_autograd_graphed_fused_adam_ms`` the same with ``torch.optim.Adam(fused=True)``.
+``train_step_autograd_graphed_fused_adam_ms`` the same with ``torch.optim.Adam(fused=True)``
+(``..._saved_ms``: also with ``backward="saved"``). ``saving_forward_ms`` and
+``saved_backward_call_ms`` time the opt-in saved-layer pair (the forward keeps the hidden
+layers, 3 KB per point; the backward reads them instead of re-running the forward).
 ``train_step_no_coordinate_grad_ms`` is the fused step without the coordinate gradient, a
 labelled variant only.
 
@@ -255,6 +258,41 @@ def main() -> None:
         log(f"backward call {args.train_points} pts: {bwd_ms * 1e3:.1f} us (GPU events over the calls)")
         return
 
+    # ---- the saved-layer pair (opt-in "saved" mode): a forward that keeps the hidden layers
+    # (3 KB per point) and a backward that reads them instead of re-running the forward. Checked
+    # bitwise against the pair above first; timed the same way, each call alone.
+    ext = load_extension()
+    gu_flat, gl_flat = gu.reshape(-1).contiguous(), gl.reshape(-1).contiguous()
+    ref_u, ref_lap = fused_forward_laplacian(x_train, params)
+    saved_u, saved_lap, saved_layers = ext._forward_saving(x_train, params, 2)
+    ref_gp, ref_gx = ext._backward(x_train, params, gu_flat, gl_flat, True, 6)
+    saved_gp, saved_gx = ext._backward(x_train, params, gu_flat, gl_flat, True, 6, saved_layers)
+    if not (torch.equal(saved_u, ref_u) and torch.equal(saved_lap, ref_lap)
+            and torch.equal(saved_gp, ref_gp) and torch.equal(saved_gx, ref_gx)):
+        raise SystemExit("the saved-layer pair differs from the forward and backward calls")
+
+    def forward_train_step():
+        fused_forward_laplacian(x_train, params)
+
+    def saving_forward_step():
+        ext._forward_saving(x_train, params, 2)
+
+    def saved_backward_step():
+        ext._backward(x_train, params, gu_flat, gl_flat, True, 6, saved_layers)
+
+    pair_ms = {}
+    for name, fn in (("forward", forward_train_step), ("saving_forward", saving_forward_step),
+                     ("saved_backward", saved_backward_step)):
+        for _ in range(args.warmup):
+            fn()
+        _, gpu = _timed(fn, args.steps, torch)
+        pair_ms[name] = gpu / args.steps
+    del saved_layers
+    log(f"saved-layer pair {args.train_points} pts: saving forward {pair_ms['saving_forward'] * 1e3:.1f} us "
+        f"(forward {pair_ms['forward'] * 1e3:.1f} us), saved-layer backward {pair_ms['saved_backward'] * 1e3:.1f} us "
+        f"(backward {bwd_ms * 1e3:.1f} us); forward + backward {(pair_ms['forward'] + bwd_ms) * 1e3:.1f} us, "
+        f"saved pair {(pair_ms['saving_forward'] + pair_ms['saved_backward']) * 1e3:.1f} us; bitwise the same results")
+
     # ---- training step (a): the reference's step through the drop-in API ----
     # fused forward (autograd.Function) + mean((Lap u - f)^2) + fused backward + torch Adam
     # (/root/reference/benchmarks/benchmark_training.py:41-60). train_step_autograd_ms runs it
@@ -292,7 +330,7 @@ def main() -> None:
     # the same steps run eagerly from the same weights (the loss each step, rtol 1e-4, and the
     # weights after); a graph that replays wrongly is not timed (the field is null and
     # train_step_autograd_graphed_note says why).
-    def autograd_graph_timing(fused_adam: bool):
+    def autograd_graph_timing(fused_adam: bool, mode: str = "cuda"):
         def make():
             torch.manual_seed(0)
             model = build_mlp(DEFAULT_POISSON_MLP).to(device)
@@ -301,7 +339,7 @@ def main() -> None:
 
         def loss_of(model):
             def loss_fn():
-                _, lap_t = fused_laplacian(model, x_train)
+                _, lap_t = fused_laplacian(model, x_train, backward=mode)
                 return (lap_t - source).pow(2).mean()
             return loss_fn
 
@@ -331,17 +369,21 @@ def main() -> None:
         total_ms, _ = _timed(replay, args.steps, torch)
         return total_ms / args.steps, "10 replays checked against eager steps (loss rtol 1e-4, weights)"
 
-    def checked_graph_timing(fused_adam: bool):
+    def checked_graph_timing(fused_adam: bool, mode: str = "cuda"):
         try:
-            return autograd_graph_timing(fused_adam)
+            return autograd_graph_timing(fused_adam, mode)
         except RuntimeError as err:  # a capture this torch build refuses: reported, not fatal
             return None, f"capture failed: {err}"
 
     autograd_graph_ms, autograd_graph_note = checked_graph_timing(False)
     # labelled variant: the same with torch.optim.Adam(fused=True) (one optimizer kernel)
     autograd_graph_fused_ms, autograd_graph_fused_note = checked_graph_timing(True)
+    # labelled variant: the same with backward="saved" (the forward keeps 3 KB per point)
+    autograd_graph_saved_ms, autograd_graph_saved_note = checked_graph_timing(True, "saved")
     for label, ms, note in (("foreach Adam", autograd_graph_ms, autograd_graph_note),
-                            ("Adam(fused=True)", autograd_graph_fused_ms, autograd_graph_fused_note)):
+                            ("Adam(fused=True)", autograd_graph_fused_ms, autograd_graph_fused_note),
+                            ("Adam(fused=True), backward='saved'", autograd_graph_saved_ms,
+                             autograd_graph_saved_note)):
         if ms is None:
             log(f"train step (autograd drop-in, whole step in a HIP graph, {label}): not timed, {note}")
         else:
@@ -489,6 +531,10 @@ def main() -> None:
         "train_step_autograd_graphed_note": autograd_graph_note,
         "train_step_autograd_graphed_fused_adam_ms": (None if autograd_graph_fused_ms is None
                                                       else round(autograd_graph_fused_ms, 5)),
+        "train_step_autograd_graphed_fused_adam_saved_ms": (None if autograd_graph_saved_ms is None
+                                                            else round(autograd_graph_saved_ms, 5)),
+        "saving_forward_ms": round(pair_ms["saving_forward"], 5),
+        "saved_backward_call_ms": round(pair_ms["saved_backward"], 5),
         "backward_call_ms": round(bwd_ms, 5),
         "gpu_clock_mhz": clock,
         "roofline": roofline,

@@ -101,11 +101,45 @@ std::vector<torch::Tensor> fused_forward_laplacian_backward(torch::Tensor coordi
 // upstream gradient may be None (zero, so no zeros tensor is made), and grad_coordinates is
 // computed only when want_coordinates is set (otherwise None is returned and nothing is
 // written). Same checks and kernels as fused_forward_laplacian_backward.
+// The forward of the autograd glue's "saved" mode: (u, Laplacian, saved layers), the last an
+// opaque uint8 buffer of fhoad_saved_layers_size(batch) bytes for backward_for_autograd.
+std::vector<torch::Tensor> forward_saving(torch::Tensor coordinates, torch::Tensor parameters,
+                                          int64_t version) {
+  TORCH_CHECK(version >= 0 && version <= 5, "version must be 0 to 5");
+  check_inputs(coordinates, parameters);
+  const c10::DeviceGuard device_guard(coordinates.device());
+  const int64_t batch = coordinates.size(0);
+  auto output = torch::empty({batch, 1}, coordinates.options());
+  auto laplacian = torch::empty({batch, 1}, coordinates.options());
+  const size_t saved_bytes = fhoad_saved_layers_size(batch);
+  auto saved = torch::empty({static_cast<int64_t>(saved_bytes)},
+                            coordinates.options().dtype(torch::kUInt8));
+  if (batch == 0) {
+    return {output, laplacian, saved};
+  }
+  check_status(fhoad_forward_laplacian_saving(
+      coordinates.data_ptr<float>(), parameters.data_ptr<float>(), output.data_ptr<float>(),
+      laplacian.data_ptr<float>(), saved.data_ptr(), saved_bytes, batch,
+      static_cast<int>(version), current_stream(coordinates)));
+  return {output, laplacian, saved};
+}
+
+// saved: forward_saving's buffer for the same coordinates and parameters (the backward then
+// reads the hidden layers instead of re-running the forward), or None.
 std::vector<c10::optional<torch::Tensor>> backward_for_autograd(
     torch::Tensor coordinates, torch::Tensor parameters, c10::optional<torch::Tensor> grad_output,
-    c10::optional<torch::Tensor> grad_laplacian, bool want_coordinates, int64_t version) {
+    c10::optional<torch::Tensor> grad_laplacian, bool want_coordinates, int64_t version,
+    c10::optional<torch::Tensor> saved) {
   TORCH_CHECK(version >= 1 && version <= 6, "backward version must be 1 to 6");
   check_inputs(coordinates, parameters);
+  if (saved.has_value()) {
+    TORCH_CHECK(saved->is_cuda() && saved->is_contiguous() && saved->scalar_type() == torch::kUInt8,
+                "saved layers must be a contiguous uint8 CUDA tensor");
+    TORCH_CHECK(saved->device() == coordinates.device(),
+                "saved layers must be on the coordinates' device");
+    TORCH_CHECK(static_cast<size_t>(saved->numel()) >= fhoad_saved_layers_size(coordinates.size(0)),
+                "saved layers do not cover the batch");
+  }
   for (const auto* grad : {&grad_output, &grad_laplacian}) {
     if (!grad->has_value()) continue;
     const torch::Tensor& g = **grad;
@@ -126,13 +160,21 @@ std::vector<c10::optional<torch::Tensor>> backward_for_autograd(
   const size_t workspace_bytes = fhoad_backward_workspace_size(batch);
   auto workspace = torch::empty({static_cast<int64_t>(workspace_bytes)},
                                 coordinates.options().dtype(torch::kUInt8));
-  check_status(fhoad_forward_laplacian_backward(
-      coordinates.data_ptr<float>(), parameters.data_ptr<float>(),
-      grad_output.has_value() ? grad_output->data_ptr<float>() : nullptr,
-      grad_laplacian.has_value() ? grad_laplacian->data_ptr<float>() : nullptr,
-      grad_parameters.data_ptr<float>(),
-      want_coordinates ? grad_coordinates->data_ptr<float>() : nullptr, workspace.data_ptr(),
-      workspace_bytes, batch, static_cast<int>(version), current_stream(coordinates)));
+  const float* gu = grad_output.has_value() ? grad_output->data_ptr<float>() : nullptr;
+  const float* gl = grad_laplacian.has_value() ? grad_laplacian->data_ptr<float>() : nullptr;
+  float* gx = want_coordinates ? grad_coordinates->data_ptr<float>() : nullptr;
+  if (saved.has_value()) {
+    check_status(fhoad_forward_laplacian_backward_saved(
+        coordinates.data_ptr<float>(), parameters.data_ptr<float>(), saved->data_ptr(),
+        static_cast<size_t>(saved->numel()), gu, gl, grad_parameters.data_ptr<float>(), gx,
+        workspace.data_ptr(), workspace_bytes, batch, static_cast<int>(version),
+        current_stream(coordinates)));
+  } else {
+    check_status(fhoad_forward_laplacian_backward(
+        coordinates.data_ptr<float>(), parameters.data_ptr<float>(), gu, gl,
+        grad_parameters.data_ptr<float>(), gx, workspace.data_ptr(), workspace_bytes, batch,
+        static_cast<int>(version), current_stream(coordinates)));
+  }
   return {grad_parameters, grad_coordinates};
 }
 
@@ -211,7 +253,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
              "optional coordinate gradient",
              pybind11::arg("coordinates"), pybind11::arg("parameters"),
              pybind11::arg("grad_output"), pybind11::arg("grad_laplacian"),
-             pybind11::arg("want_coordinates"), pybind11::arg("version") = 6);
+             pybind11::arg("want_coordinates"), pybind11::arg("version") = 6,
+             pybind11::arg("saved") = pybind11::none());
+  module.def("_forward_saving", &forward_saving,
+             "Forward that also keeps the hidden layers' outputs for _backward(saved=...)",
+             pybind11::arg("coordinates"), pybind11::arg("parameters"),
+             pybind11::arg("version") = 2);
   module.def("fused_forward_laplacian", &fused_forward_laplacian,
              "Fixed MLP forward pass and input Laplacian (MI355X HIP kernel)",
              pybind11::arg("coordinates"), pybind11::arg("parameters"),

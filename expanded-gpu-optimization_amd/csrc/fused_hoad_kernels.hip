@@ -524,6 +524,45 @@ __device__ __forceinline__ float row_reduce_scatter16(const float (&v)[16], int 
 }
 
 // ---------------------------------------------------------------------------------------------
+// Layer outputs saved by the forward for a backward that reads them instead of re-running the
+// forward (fhoad_forward_laplacian_saving, fhoad_forward_laplacian_backward_saved): per
+// 16-point tile t, hidden layer l (0..2 for layers 1..3), row block mb and jet component c, the
+// 64 lanes' f4 in lane order. Lane (m, g)'s f4 holds rows 16 mb + 4 g + r (r = 0..3) at point
+// 16 t + m, the MFMA accumulator layout every kernel here keeps a layer's output in, so each
+// store and load moves 1 KB per wave contiguously. 3,072 f4 (49,152 bytes) per tile.
+constexpr int64_t kSavedF4PerTile = 3 * 16 * kWave;
+__device__ __forceinline__ int64_t saved_index(int64_t tile, int layer, int mb, int c, int lane) {
+  return ((tile * 3 + layer) * 16 + 4 * mb + c) * kWave + lane;
+}
+
+// The forward writes the saved layers as non-temporal stores (about 2 us less per 64K call than
+// plain stores, measured); the backward reads them with plain loads (non-temporal loads
+// measured about 7 us slower per 64K call).
+__device__ __forceinline__ void store_saved(f4* __restrict__ saved, int64_t index, f4 value) {
+  __builtin_nontemporal_store(value, &saved[index]);
+}
+
+// One hidden layer's saved output of a 16-point tile into the accumulator layout (zeros for a
+// tile past the saved ones).
+__device__ __forceinline__ void load_saved_layer(const f4* __restrict__ saved, int64_t tile,
+                                                 int64_t saved_tiles, int layer, int lane,
+                                                 f4 (&h)[4][4]) {
+  if (tile < saved_tiles) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) h[mb][c] = saved[saved_index(tile, layer, mb, c, lane)];
+    }
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) h[mb][c] = f4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Forward kernel (replaces fused_forward_laplacian_tiled_kernel<2>,
 // /root/reference/csrc/fused_residual.cu:157-295). A grid of at most one workgroup per CU
 // stages the weights once, then every wave walks 16-point tiles: tile t < whole goes to
@@ -557,11 +596,12 @@ __device__ __forceinline__ void quad_sync(unsigned* flag, unsigned target) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-template <int kWaves>
+// kSave: also write each tile's hidden-layer outputs to `saved` (saved_index).
+template <int kWaves, bool kSave>
 __global__ void __launch_bounds__(kWaves * kWave)
 forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                float* __restrict__ output, float* __restrict__ laplacian, int64_t batch,
-               int64_t whole, int64_t tiles) {
+               int64_t whole, int64_t tiles, f4* __restrict__ saved) {
   __shared__ __attribute__((aligned(16))) float s_wa[3 * kOperandLayerF4 * 4];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ f4 s_x[2][4][4][kWave];  // split tiles: [buffer][wave q][component][lane], 32 KB
@@ -623,6 +663,10 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
         }
         f4 mine[4];
         tanh_jet4(acc, mine);
+        if (kSave) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) store_saved(saved, saved_index(t, layer, q, c, lane), mine[c]);
+        }
         f4 (*buf)[4][kWave] = s_x[phase];
         phase ^= 1;
 #pragma unroll
@@ -680,6 +724,13 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
       hidden_product_native(wa_lane + layer * kOperandLayerF4, h, bias, acc, first);
       if (layer < 2) first = wa_lane[(layer + 1) * kOperandLayerF4];
       apply_tanh_jet(acc, h);
+      if (kSave) {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) store_saved(saved, saved_index(tile, layer, mb, c, lane), h[mb][c]);
+        }
+      }
     }
     // Take delivery of the next coordinates here, before this tile's stores: a wait at the
     // top of the next tile would also wait for those stores (they sit behind a branch, so the
@@ -724,10 +775,11 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
 // order, so both kernels give bitwise the same results.
 constexpr int kSplitWaves = 4;
 
+template <bool kSave>
 __global__ void __launch_bounds__(kSplitWaves * kWave)
 forward_split_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                      float* __restrict__ output, float* __restrict__ laplacian, int64_t batch,
-                     int64_t tiles) {
+                     int64_t tiles, f4* __restrict__ saved) {
   __shared__ f4 s_h[2][kSplitWaves][4][kWave];  // [buffer][wave][component][lane], 32 KB
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   stage_small(params, s_small, threadIdx.x, kSplitWaves * kWave);
@@ -793,6 +845,10 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
           mine[2][r] = sl[r] * acc[2][r];
           mine[3][r] = sl[r] * __builtin_fmaf(v[r], q, acc[3][r]);
         }
+      }
+      if (kSave) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) store_saved(saved, saved_index(tile, layer, w, c, lane), mine[c]);
       }
       f4 (*buf)[4][kWave] = s_h[phase];
       phase ^= 1;
@@ -1631,12 +1687,19 @@ __device__ __forceinline__ void split_tile(const float* s_w, const float* s_smal
 //
 // kLoss: grad_output and grad_laplacian are unused and the seed comes from `seed` (above);
 // grad_coordinates may be null.
-template <bool kLoss, bool kRest>
+// kSaved (backward call only): interior tiles read h1, h2, h3 from `saved`, written by the
+// saving forward (saved_index; saved_tiles 16-point tiles), instead of re-running the forward.
+// A wave whose 16-point tile lies past the batch takes zeros: its upstream gradients are zero,
+// so every product with its h is zero either way. Split tiles past the last whole round still
+// re-run the forward.
+template <bool kLoss, bool kRest, bool kSaved>
 __global__ void __launch_bounds__(kBwdWaves * kWave, 1)
 backward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                 const float* __restrict__ grad_output, const float* __restrict__ grad_laplacian,
                 float* __restrict__ grad_coordinates, float* __restrict__ partials,
-                int64_t batch, int64_t whole, int64_t tiles, int slots, LossSeed seed) {
+                int64_t batch, int64_t whole, int64_t tiles, int slots, LossSeed seed,
+                const f4* __restrict__ saved, int64_t saved_tiles) {
+  static_assert(!(kLoss && kSaved), "the fused step computes its forward once; nothing to read");
   constexpr int kStageFloats =
       kRest && kSplitScratchFloats > 4 * kSPlane ? kSplitScratchFloats : 4 * kSPlane;
   __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
@@ -1689,7 +1752,24 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     // copies a tile, where the two paths' accumulators met at the loop's back edge.
     int64_t tile = slot;
     const int64_t interior_end = kLoss ? std::min<int64_t>(tiles, seed.interior_tiles) : tiles;
-    for (; tile < (kRest ? whole : interior_end); tile += slots) {
+    const int64_t loop_end = kRest ? whole : interior_end;
+    // Hidden-layer outputs of the current tile. With kSaved each layer of the next tile is read
+    // where this tile's copy dies in the walk back (layer 3 after W3^T zbar3, layer 2 after
+    // W2^T zbar2, layer 1 at the end), so the reads spread over the tile: read at each tile's
+    // start, the waves of all CUs asked for their 48 KB at once and waited out that burst.
+    // (Reading a slot's first tile before the weight staging measured no faster.)
+    f4 h1[4][4], h2[4][4], h3[4][4];
+    if constexpr (kSaved) {
+      if (tile < loop_end) {
+        const int64_t saved_tile = kBwdWaves * tile + w;
+        load_saved_layer(saved, saved_tile, saved_tiles, 2, lane, h3);
+        load_saved_layer(saved, saved_tile, saved_tiles, 1, lane, h2);
+        load_saved_layer(saved, saved_tile, saved_tiles, 0, lane, h1);
+      }
+    }
+    for (; tile < loop_end; tile += slots) {
+      const bool has_next = tile + slots < loop_end;
+      const int64_t next_saved_tile = kBwdWaves * (tile + slots) + w;
       keep_lds_reads_in_loop();
       const int m_pick = opaque(m);  // row_reduce_scatter16's lane masks stay inside the tile
       const TileInputs in = next;
@@ -1703,15 +1783,16 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       float gu = kLoss ? 0.f : in.a, gl = kLoss ? 0.f : in.b;
       const float f = kLoss ? in.a : 0.f;
 
-      // ---- 1. forward recompute, keeping each hidden layer's tanh-jet output ----
-      f4 h1[4][4], h2[4][4], h3[4][4];
-      {
-        f4 h0[4][4];
-        layer0_forward(s_small, g, x0, x1, h0);
-        forward_layer(s_small, s_w + opaque(rows_off), 0, g, h0, h1);
+      // ---- 1. forward recompute (kSaved: read ahead, above and in the walk back) ----
+      if constexpr (!kSaved) {
+        {
+          f4 h0[4][4];
+          layer0_forward(s_small, g, x0, x1, h0);
+          forward_layer(s_small, s_w + opaque(rows_off), 0, g, h0, h1);
+        }
+        forward_layer(s_small, s_w + opaque(rows_off), 1, g, h1, h2);
+        forward_layer(s_small, s_w + opaque(rows_off), 2, g, h2, h3);
       }
-      forward_layer(s_small, s_w + opaque(rows_off), 1, g, h1, h2);
-      forward_layer(s_small, s_w + opaque(rows_off), 2, g, h2, h3);
 
       if (kLoss) {
         // lap = w_out . L in the forward kernel's order, then the seed.
@@ -1763,12 +1844,18 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       stage_and_dw_h(h3, h2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
                      s_stage + opaque(stage_even_off), s_stage + opaque(stage_odd_off), w);
       adjoint_through(s_w + opaque(cols_off) + 2 * kPlane, h3, h2);
+      if constexpr (kSaved) {
+        if (has_next) load_saved_layer(saved, next_saved_tile, saved_tiles, 2, lane, h3);
+      }
 
       // ---- 4. hidden layer 2: dW2 from (zbar2, h1), then W2^T zbar2 into layer 1's adjoint ----
       stage_and_dw_h(h2, h1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
                      s_stage + opaque(stage_even_off), s_stage + opaque(stage_odd_off), w);
       deliver(next);  // the next tile's inputs, before this tile's stores
       adjoint_through(s_w + opaque(cols_off) + kPlane, h2, h1);
+      if constexpr (kSaved) {
+        if (has_next) load_saved_layer(saved, next_saved_tile, saved_tiles, 1, lane, h2);
+      }
 
       // ---- 5. hidden layer 1: dW1 from (zbar1, h0), h0 rebuilt with its (v', s') ----
       f4 v0[4], s0[4];
@@ -1812,6 +1899,9 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         acc.w0x += row_reduce_scatter16(tx, m_pick);
         acc.w0y += row_reduce_scatter16(ty, m_pick);
         acc.b0 += row_reduce_scatter16(tb, m_pick);
+        if constexpr (kSaved) {
+          if (has_next) load_saved_layer(saved, next_saved_tile, saved_tiles, 0, lane, h1);
+        }
         gx0 = sum_lane_groups(gx0);
         gx1 = sum_lane_groups(gx1);
         if (g == 0 && active && grad_coordinates != nullptr) {
@@ -2225,10 +2315,11 @@ int current_device_cus(int* cus) {
   return FHOAD_SUCCESS;
 }
 
-// The workspace must be 16-byte aligned (part of the ABI: hipMalloc and torch allocations are).
-int check_workspace_alignment(const void* workspace) {
+// Workspaces and saved-layer buffers must be 16-byte aligned (part of the ABI: hipMalloc and
+// torch allocations are).
+int check_workspace_alignment(const void* workspace, const char* what = "workspace") {
   if (reinterpret_cast<uintptr_t>(workspace) % alignof(f4) != 0) {
-    return fail(FHOAD_ERROR_MISALIGNED, "workspace must be 16-byte aligned");
+    return fail(FHOAD_ERROR_MISALIGNED, "%s must be 16-byte aligned", what);
   }
   return FHOAD_SUCCESS;
 }
@@ -2333,7 +2424,7 @@ int noalloc_scratch(void** out) {
 // Backward call on a workspace of `workspace_bytes` bytes (checked by the caller).
 int launch_backward(const float* coordinates, const float* parameters, const float* grad_output,
                     const float* grad_laplacian, float* grad_parameters, float* grad_coordinates,
-                    void* workspace, int64_t batch, hipStream_t hs);
+                    void* workspace, int64_t batch, hipStream_t hs, const void* saved = nullptr);
 
 }  // namespace
 }  // namespace fhoad
@@ -2358,6 +2449,46 @@ extern "C" const char* fhoad_status_string(int status) {
 
 extern "C" const char* fhoad_last_error(void) { return g_last_error; }
 
+namespace fhoad {
+namespace {
+
+// The forward launch shared by fhoad_forward_laplacian and fhoad_forward_laplacian_saving
+// (kSave: the kernels also write the hidden-layer outputs to `saved`). batch > 0.
+template <bool kSave>
+int launch_forward(const float* coordinates, const float* parameters, float* output,
+                   float* laplacian, void* saved, int64_t batch, hipStream_t hs) {
+  int cus = 0;
+  if (int st = current_device_cus(&cus)) return st;
+  const int64_t tiles = (batch + kTile - 1) / kTile;
+  const int grid = static_cast<int>(std::min<int64_t>(tiles, cus));
+  f4* saved_f4 = static_cast<f4*>(saved);
+  // Below kSplitTilesPerCu tiles per CU the split kernel runs each tile on a CU's 4 SIMDs.
+  // FUSED_HOAD_FWD_SPLIT=0 / 1 (experiment knob, read per call) forces either kernel.
+  const char* split_env = std::getenv("FUSED_HOAD_FWD_SPLIT");
+  const bool split = split_env ? std::atoi(split_env) != 0 : tiles <= kSplitTilesPerCu * cus;
+  if (split) {
+    const int split_grid = static_cast<int>(std::min<int64_t>(tiles, kSplitTilesPerCu * cus));
+    hipLaunchKernelGGL(forward_split_kernel<kSave>, dim3(split_grid), dim3(kSplitWaves * kWave), 0,
+                       hs, coordinates, parameters, output, laplacian, batch, tiles, saved_f4);
+    return check_launch("forward_split_kernel");
+  }
+  const int64_t whole = forward_whole_tiles(tiles, grid);
+  // FUSED_HOAD_FWD_WAVES=8 (experiment knob, read per call) selects 8 waves per workgroup.
+  const char* env = std::getenv("FUSED_HOAD_FWD_WAVES");
+  if (env && std::atoi(env) == 8) {
+    hipLaunchKernelGGL((forward_kernel<8, kSave>), dim3(grid), dim3(8 * kWave), 0, hs, coordinates,
+                       parameters, output, laplacian, batch, whole, tiles, saved_f4);
+  } else {
+    hipLaunchKernelGGL((forward_kernel<kFwdWaves, kSave>), dim3(grid), dim3(kFwdWaves * kWave), 0,
+                       hs, coordinates, parameters, output, laplacian, batch, whole, tiles,
+                       saved_f4);
+  }
+  return check_launch("forward_kernel");
+}
+
+}  // namespace
+}  // namespace fhoad
+
 extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* parameters,
                                        float* output, float* laplacian, int64_t batch,
                                        int version, void* stream) {
@@ -2367,32 +2498,33 @@ extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* pa
   if (!coordinates || !parameters || !output || !laplacian) {
     return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
   }
-  int cus = 0;
-  if (int st = current_device_cus(&cus)) return st;
-  const int64_t tiles = (batch + kTile - 1) / kTile;
-  const int grid = static_cast<int>(std::min<int64_t>(tiles, cus));
-  const hipStream_t hs = static_cast<hipStream_t>(stream);
-  // Below kSplitTilesPerCu tiles per CU the split kernel runs each tile on a CU's 4 SIMDs.
-  // FUSED_HOAD_FWD_SPLIT=0 / 1 (experiment knob, read per call) forces either kernel.
-  const char* split_env = std::getenv("FUSED_HOAD_FWD_SPLIT");
-  const bool split = split_env ? std::atoi(split_env) != 0 : tiles <= kSplitTilesPerCu * cus;
-  if (split) {
-    const int split_grid = static_cast<int>(std::min<int64_t>(tiles, kSplitTilesPerCu * cus));
-    hipLaunchKernelGGL(forward_split_kernel, dim3(split_grid), dim3(kSplitWaves * kWave), 0, hs,
-                       coordinates, parameters, output, laplacian, batch, tiles);
-    return check_launch("forward_split_kernel");
+  return launch_forward<false>(coordinates, parameters, output, laplacian, nullptr, batch,
+                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t fhoad_saved_layers_size(int64_t batch) {
+  if (batch <= 0) return 0;
+  return static_cast<size_t>((batch + kTile - 1) / kTile) * kSavedF4PerTile * sizeof(f4);
+}
+
+extern "C" int fhoad_forward_laplacian_saving(const float* coordinates, const float* parameters,
+                                              float* output, float* laplacian, void* saved,
+                                              size_t saved_bytes, int64_t batch, int version,
+                                              void* stream) {
+  if (version < 0 || version > 5) return fail(FHOAD_ERROR_INVALID_VERSION, "version must be 0 to 5");
+  if (batch < 0) return fail(FHOAD_ERROR_INVALID_VALUE, "batch must be non-negative");
+  if (batch == 0) return FHOAD_SUCCESS;
+  if (!coordinates || !parameters || !output || !laplacian) {
+    return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
   }
-  const int64_t whole = forward_whole_tiles(tiles, grid);
-  // FUSED_HOAD_FWD_WAVES=8 (experiment knob, read per call) selects 8 waves per workgroup.
-  const char* env = std::getenv("FUSED_HOAD_FWD_WAVES");
-  if (env && std::atoi(env) == 8) {
-    hipLaunchKernelGGL(forward_kernel<8>, dim3(grid), dim3(8 * kWave), 0, hs, coordinates,
-                       parameters, output, laplacian, batch, whole, tiles);
-  } else {
-    hipLaunchKernelGGL(forward_kernel<kFwdWaves>, dim3(grid), dim3(kFwdWaves * kWave), 0, hs,
-                       coordinates, parameters, output, laplacian, batch, whole, tiles);
+  const size_t needed = fhoad_saved_layers_size(batch);
+  if (!saved || saved_bytes < needed) {
+    return fail(FHOAD_ERROR_WORKSPACE, "saved-layer buffer holds %zu bytes, %zu needed", saved_bytes,
+                needed);
   }
-  return check_launch("forward_kernel");
+  if (int st = check_workspace_alignment(saved, "saved-layer buffer")) return st;
+  return launch_forward<true>(coordinates, parameters, output, laplacian, saved, batch,
+                              static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t fhoad_backward_workspace_size(int64_t batch) {
@@ -2460,13 +2592,50 @@ extern "C" int fhoad_forward_laplacian_backward_noalloc(
                          grad_coordinates, device_scratch, batch, hs);
 }
 
+extern "C" int fhoad_forward_laplacian_backward_saved(
+    const float* coordinates, const float* parameters, const void* saved, size_t saved_bytes,
+    const float* grad_output, const float* grad_laplacian, float* grad_parameters,
+    float* grad_coordinates, void* workspace, size_t workspace_bytes, int64_t batch, int version,
+    void* stream) {
+  if (version < 1 || version > 6) {
+    return fail(FHOAD_ERROR_INVALID_VERSION, "backward version must be 1 to 6");
+  }
+  if (batch < 0) return fail(FHOAD_ERROR_INVALID_VALUE, "batch must be non-negative");
+  if (!parameters || !grad_parameters) return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  if (batch == 0) {
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((kParameterCount + 255) / 256), dim3(256), 0, hs,
+                       grad_parameters, static_cast<int64_t>(kParameterCount));
+    return check_launch("fill_zero_kernel");
+  }
+  if (!coordinates) return fail(FHOAD_ERROR_INVALID_VALUE, "null device pointer");
+  const size_t saved_needed = fhoad_saved_layers_size(batch);
+  if (!saved || saved_bytes < saved_needed) {
+    return fail(FHOAD_ERROR_WORKSPACE, "saved-layer buffer holds %zu bytes, %zu needed",
+                saved_bytes, saved_needed);
+  }
+  if (int st = check_workspace_alignment(saved, "saved-layer buffer")) return st;
+  const size_t needed = fhoad_backward_workspace_size(batch);
+  if (!workspace || workspace_bytes < needed) {
+    return fail(FHOAD_ERROR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes,
+                needed);
+  }
+  if (int st = check_workspace_alignment(workspace)) return st;
+  return launch_backward(coordinates, parameters, grad_output, grad_laplacian, grad_parameters,
+                         grad_coordinates, workspace, batch, hs, saved);
+}
+
 namespace fhoad {
 namespace {
 
+// saved: the saving forward's layer outputs for this batch (fhoad_saved_layers_size bytes), or
+// null to re-run the forward. Batches the small-batch kernel takes re-run it either way.
 int launch_backward(const float* coordinates, const float* parameters, const float* grad_output,
                     const float* grad_laplacian, float* grad_parameters, float* grad_coordinates,
-                    void* workspace, int64_t batch, hipStream_t hs) {
+                    void* workspace, int64_t batch, hipStream_t hs, const void* saved) {
   float* partials = static_cast<float*>(workspace);
+  const f4* saved_f4 = static_cast<const f4*>(saved);
+  const int64_t saved_tiles = (batch + kTile - 1) / kTile;
   int slots = 0, grid = 0;
   if (use_split_backward(batch, 0)) {
     const int64_t tiles = split_tiles(batch);
@@ -2480,16 +2649,27 @@ int launch_backward(const float* coordinates, const float* parameters, const flo
     slots = backward_slots(batch);
     if (int st = backward_grid(slots, &grid)) return st;
     const InteriorTiles it = interior_tiles_for(batch, slots);
-    if (it.whole != it.total) {
-      hipLaunchKernelGGL((backward_kernel<false, true>), dim3(grid), dim3(kBwdWaves * kWave), 0,
-                         hs, coordinates, parameters, grad_output, grad_laplacian,
-                         grad_coordinates, partials, batch, it.whole, it.total, slots,
-                         LossSeed{});
+    const dim3 block(kBwdWaves * kWave);
+    if (it.whole != it.total && saved) {
+      hipLaunchKernelGGL((backward_kernel<false, true, true>), dim3(grid), block, 0, hs,
+                         coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
+                         partials, batch, it.whole, it.total, slots, LossSeed{}, saved_f4,
+                         saved_tiles);
+    } else if (it.whole != it.total) {
+      hipLaunchKernelGGL((backward_kernel<false, true, false>), dim3(grid), block, 0, hs,
+                         coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
+                         partials, batch, it.whole, it.total, slots, LossSeed{}, nullptr,
+                         int64_t{0});
+    } else if (saved) {
+      hipLaunchKernelGGL((backward_kernel<false, false, true>), dim3(grid), block, 0, hs,
+                         coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
+                         partials, batch, it.whole, it.total, slots, LossSeed{}, saved_f4,
+                         saved_tiles);
     } else {
-      hipLaunchKernelGGL((backward_kernel<false, false>), dim3(grid), dim3(kBwdWaves * kWave), 0,
-                         hs, coordinates, parameters, grad_output, grad_laplacian,
-                         grad_coordinates, partials, batch, it.whole, it.total, slots,
-                         LossSeed{});
+      hipLaunchKernelGGL((backward_kernel<false, false, false>), dim3(grid), block, 0, hs,
+                         coordinates, parameters, grad_output, grad_laplacian, grad_coordinates,
+                         partials, batch, it.whole, it.total, slots, LossSeed{}, nullptr,
+                         int64_t{0});
     }
     if (int st = check_launch("backward_kernel")) return st;
   }
@@ -2551,13 +2731,13 @@ extern "C" int fhoad_poisson_adam_step(const float* coordinates, const float* so
     if (int st = check_launch("backward_split_kernel")) return st;
   } else {
     if (it.whole != it.total) {
-      hipLaunchKernelGGL((backward_kernel<true, true>), dim3(grid), dim3(kBwdWaves * kWave), 0, hs,
-                         coordinates, parameters, nullptr, nullptr, grad_coordinates, partials,
-                         batch, it.whole, tiles, slots, seed);
+      hipLaunchKernelGGL((backward_kernel<true, true, false>), dim3(grid), dim3(kBwdWaves * kWave),
+                         0, hs, coordinates, parameters, nullptr, nullptr, grad_coordinates,
+                         partials, batch, it.whole, tiles, slots, seed, nullptr, int64_t{0});
     } else {
-      hipLaunchKernelGGL((backward_kernel<true, false>), dim3(grid), dim3(kBwdWaves * kWave), 0,
-                         hs, coordinates, parameters, nullptr, nullptr, grad_coordinates,
-                         partials, batch, it.whole, tiles, slots, seed);
+      hipLaunchKernelGGL((backward_kernel<true, false, false>), dim3(grid), dim3(kBwdWaves * kWave),
+                         0, hs, coordinates, parameters, nullptr, nullptr, grad_coordinates,
+                         partials, batch, it.whole, tiles, slots, seed, nullptr, int64_t{0});
     }
     if (int st = check_launch("backward_kernel")) return st;
   }

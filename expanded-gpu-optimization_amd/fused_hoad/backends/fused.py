@@ -3,7 +3,9 @@
 Fixed to the Poisson contract (2 -> 64x4 -> 1 tanh, FP32, on the GPU). The forward is one
 kernel; the backward is the fused HIP kernel pair (default) or, when asked for by name, the
 reference's PyTorch recompute-and-differentiate path. Behaviour follows
-/root/reference/src/fused_hoad/backends/fused.py:24-138.
+/root/reference/src/fused_hoad/backends/fused.py:24-138. One mode the reference does not have,
+``"saved"``, keeps the forward's hidden-layer outputs (3 KB per point) so that the HIP
+backward reads them instead of re-running the forward.
 """
 
 from __future__ import annotations
@@ -28,7 +30,9 @@ from fused_hoad.parameters import (
 )
 
 # Backward modes. Every "cuda*" name runs the same fused HIP backward (the reference's kernel
-# versions are kept as names only); "recompute" is the PyTorch reference backward.
+# versions are kept as names only); "recompute" is the PyTorch reference backward; "saved" is
+# the HIP backward reading the layer outputs the forward kept (bitwise the same gradients as
+# "cuda", with 3 KB per point held from the forward to the backward).
 _CUDA_BACKWARD_VERSIONS = {
     "cuda": 6,
     "cuda_v1": 1,
@@ -37,7 +41,9 @@ _CUDA_BACKWARD_VERSIONS = {
     "cuda_v4": 4,
     "cuda_v5": 5,
 }
-BACKWARD_MODES = (*_CUDA_BACKWARD_VERSIONS, "recompute")
+BACKWARD_MODES = (*_CUDA_BACKWARD_VERSIONS, "recompute")  # the reference's names
+SAVED_MODE = "saved"
+_ACCEPTED_MODES = (*BACKWARD_MODES, SAVED_MODE)
 
 _cache: dict[str, object] = {}
 
@@ -47,15 +53,30 @@ class FusedForwardLaplacian(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, coordinates: Tensor, parameters: Tensor, version: int, backward: str):
-        ctx.save_for_backward(coordinates, parameters)
         ctx.backward_mode = backward
+        if backward == SAVED_MODE:
+            output, laplacian, saved = load_extension()._forward_saving(coordinates, parameters, version)
+            ctx.save_for_backward(coordinates, parameters, saved)
+            return output, laplacian
+        ctx.save_for_backward(coordinates, parameters)
         return fused_forward_laplacian(coordinates, parameters, version)
 
     @staticmethod
     def backward(ctx, grad_output: Tensor, grad_laplacian: Tensor):
-        coordinates, parameters = ctx.saved_tensors
+        coordinates, parameters, *saved = ctx.saved_tensors
         needs_coordinates, needs_parameters = ctx.needs_input_grad[:2]
         mode = ctx.backward_mode
+        if mode == SAVED_MODE:
+            grad_parameters, grad_coordinates = load_extension()._backward(
+                coordinates,
+                parameters,
+                grad_output.reshape(-1).contiguous(),
+                grad_laplacian.reshape(-1).contiguous(),
+                needs_coordinates,
+                6,
+                saved[0],
+            )
+            return grad_coordinates, grad_parameters if needs_parameters else None, None, None
         if mode in _CUDA_BACKWARD_VERSIONS:
             grad_parameters, grad_coordinates = fused_forward_laplacian_backward(
                 coordinates, parameters, grad_output, grad_laplacian, _CUDA_BACKWARD_VERSIONS[mode]
@@ -83,27 +104,32 @@ class FlattenedFusedLaplacian(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, coordinates: Tensor, flat: Tensor, version: int, backward: str, *parameters: Tensor):
-        ctx.save_for_backward(coordinates, flat)
         ctx.backward_mode = backward
         ctx.set_materialize_grads(False)
+        if backward == SAVED_MODE:
+            output, laplacian, saved = load_extension()._forward_saving(coordinates, flat, version)
+            ctx.save_for_backward(coordinates, flat, saved)
+            return output, laplacian
+        ctx.save_for_backward(coordinates, flat)
         return fused_forward_laplacian(coordinates, flat, version)
 
     @staticmethod
     def backward(ctx, grad_output: Tensor | None, grad_laplacian: Tensor | None):
-        coordinates, flat = ctx.saved_tensors
+        coordinates, flat, *saved = ctx.saved_tensors
         needs_coordinates = ctx.needs_input_grad[0]
         needs_parameters = any(ctx.needs_input_grad[4:])
         if grad_output is None and grad_laplacian is None:
             return (None,) * (4 + len(POISSON_PARAMETER_LAYOUT) * 2)
         mode = ctx.backward_mode
-        if mode in _CUDA_BACKWARD_VERSIONS:
+        if mode in _CUDA_BACKWARD_VERSIONS or mode == SAVED_MODE:
             grad_flat, grad_coordinates = load_extension()._backward(
                 coordinates,
                 flat,
                 None if grad_output is None else grad_output.reshape(-1).contiguous(),
                 None if grad_laplacian is None else grad_laplacian.reshape(-1).contiguous(),
                 needs_coordinates,
-                _CUDA_BACKWARD_VERSIONS[mode],
+                _CUDA_BACKWARD_VERSIONS.get(mode, 6),
+                saved[0] if saved else None,
             )
         else:
             zeros = torch.zeros(coordinates.shape[0], 1, dtype=flat.dtype, device=flat.device)
@@ -192,10 +218,12 @@ def fused_laplacian(
     """``(u, Laplacian u)`` of the fixed Poisson MLP from one gfx950 kernel launch.
 
     ``backward`` selects the gradient path when autograd is active: any ``"cuda*"`` mode runs
-    the fused HIP backward; ``"recompute"`` runs the PyTorch reference backward.
+    the fused HIP backward; ``"recompute"`` runs the PyTorch reference backward; ``"saved"``
+    runs the fused HIP backward on the layer outputs the forward kept (3 KB per point until the
+    backward), which spares it the forward re-run and gives bitwise the same gradients.
     """
-    if backward not in BACKWARD_MODES:
-        raise ValueError(f"backward must be one of {BACKWARD_MODES}")
+    if backward not in _ACCEPTED_MODES:
+        raise ValueError(f"backward must be one of {_ACCEPTED_MODES}")
     if torch.is_grad_enabled():
         flat = flattened_poisson_parameters(model)
         if flat is not None:  # parameters are views of the packed buffer: no pack at all

@@ -111,6 +111,43 @@ int fhoad_forward_laplacian_backward_noalloc(const float* coordinates, const flo
                                              int64_t batch, int version, void* stream);
 
 /*
+ * Bytes of the saved-layer buffer fhoad_forward_laplacian_saving writes for `batch` points:
+ * 49,152 bytes (the three hidden layers' outputs, 4 jet components x 64 neurons each) per
+ * 16-point tile, ceil(batch / 16) tiles, i.e. 3 KB per point. 0 for batch <= 0.
+ */
+size_t fhoad_saved_layers_size(int64_t batch);
+
+/*
+ * fhoad_forward_laplacian that also writes the hidden layers' outputs (the forward jet after
+ * each tanh) to `saved`, for fhoad_forward_laplacian_backward_saved. output and laplacian are
+ * bitwise those of fhoad_forward_laplacian. saved must hold fhoad_saved_layers_size(batch)
+ * bytes and be 16-byte aligned; its layout is private to this library.
+ *
+ * No counterpart in the reference, whose backward always re-runs the forward: it is for
+ * autograd callers that can keep 3 KB per point between the forward and the backward.
+ */
+int fhoad_forward_laplacian_saving(const float* coordinates, const float* parameters,
+                                   float* output, float* laplacian, void* saved,
+                                   size_t saved_bytes, int64_t batch, int version, void* stream);
+
+/*
+ * fhoad_forward_laplacian_backward reading the hidden layers' outputs from `saved` (written by
+ * fhoad_forward_laplacian_saving for the same coordinates and parameters, left unchanged since)
+ * instead of re-running the forward: a third of the backward's matrix work. Same arguments,
+ * contract and workspace as fhoad_forward_laplacian_backward, and bitwise the same results.
+ * Batches of up to 12,288 points (the small-batch kernel) and the points past the last whole
+ * round of 64-point tiles re-run the forward as before.
+ *
+ * No counterpart in the reference (see fhoad_forward_laplacian_saving).
+ */
+int fhoad_forward_laplacian_backward_saved(const float* coordinates, const float* parameters,
+                                           const void* saved, size_t saved_bytes,
+                                           const float* grad_output, const float* grad_laplacian,
+                                           float* grad_parameters, float* grad_coordinates,
+                                           void* workspace, size_t workspace_bytes, int64_t batch,
+                                           int version, void* stream);
+
+/*
  * Bytes of device workspace fhoad_poisson_adam_step needs for `batch` interior and
  * `boundary_count` boundary points. 0 for batch <= 0 or boundary_count < 0.
  */

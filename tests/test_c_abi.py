@@ -41,6 +41,13 @@ def _lib() -> ctypes.CDLL:
     )
     lib.fhoad_poisson_adam_step_workspace_size.restype = ctypes.c_size_t
     lib.fhoad_poisson_adam_step_workspace_size.argtypes = [i64, i64]
+    sz = ctypes.c_size_t
+    lib.fhoad_saved_layers_size.restype = sz
+    lib.fhoad_saved_layers_size.argtypes = [i64]
+    lib.fhoad_forward_laplacian_saving.restype = ci
+    lib.fhoad_forward_laplacian_saving.argtypes = [vp, vp, vp, vp, vp, sz, i64, ci, vp]
+    lib.fhoad_forward_laplacian_backward_saved.restype = ci
+    lib.fhoad_forward_laplacian_backward_saved.argtypes = [vp, vp, vp, sz, vp, vp, vp, vp, vp, sz, i64, ci, vp]
     return lib
 
 
@@ -56,10 +63,13 @@ def test_header_declares_the_entry_points() -> None:
         "fhoad_forward_laplacian",
         "fhoad_forward_laplacian_backward",
         "fhoad_forward_laplacian_backward_noalloc",
+        "fhoad_forward_laplacian_backward_saved",
+        "fhoad_forward_laplacian_saving",
         "fhoad_last_error",
         "fhoad_parameter_count",
         "fhoad_poisson_adam_step",
         "fhoad_poisson_adam_step_workspace_size",
+        "fhoad_saved_layers_size",
         "fhoad_status_string",
     ]
 
@@ -142,6 +152,34 @@ def test_argument_errors_are_reported_before_any_device_work() -> None:
     backward = lib.fhoad_forward_laplacian_backward
     assert backward(fake, fake, fake, fake, fake, fake, odd, 1 << 30, 16, 6, None) == 3
     assert b"16-byte aligned" in lib.fhoad_last_error()
+    # the saved-layer pair: the buffer is checked (presence, size, alignment) before any launch
+    saving = lib.fhoad_forward_laplacian_saving
+    need = lib.fhoad_saved_layers_size(16)
+    assert saving(fake, fake, fake, fake, None, need, 16, 2, None) == 4
+    assert saving(fake, fake, fake, fake, fake, need - 1, 16, 2, None) == 4
+    assert b"saved-layer buffer holds" in lib.fhoad_last_error()
+    assert saving(fake, fake, fake, fake, odd, need, 16, 2, None) == 3
+    assert b"saved-layer buffer must be 16-byte aligned" in lib.fhoad_last_error()
+    assert saving(fake, fake, fake, fake, None, 0, 16, 6, None) == 1
+    assert saving(None, None, None, None, None, 0, 0, 2, None) == 0
+    saved_bwd = lib.fhoad_forward_laplacian_backward_saved
+    assert saved_bwd(fake, fake, None, need, fake, fake, fake, fake, fake, 1 << 30, 16, 6, None) == 4
+    assert saved_bwd(fake, fake, fake, need - 16, fake, fake, fake, fake, fake, 1 << 30, 16, 6, None) == 4
+    assert saved_bwd(fake, fake, odd, need, fake, fake, fake, fake, fake, 1 << 30, 16, 6, None) == 3
+    assert saved_bwd(fake, fake, fake, need, fake, fake, fake, fake, fake, 10, 16, 6, None) == 4
+    assert b"workspace holds" in lib.fhoad_last_error()
+    assert saved_bwd(fake, fake, fake, need, fake, fake, fake, fake, fake, 1 << 30, 16, 0, None) == 1
+
+
+def test_saved_layers_size() -> None:
+    """3,072 f4 (49,152 bytes) per 16-point tile: the three hidden layers' 64 neurons x 4 jet
+    components for 16 points, i.e. 3 KB per point, in whole tiles."""
+    lib = _lib()
+    assert lib.fhoad_saved_layers_size(0) == 0
+    assert lib.fhoad_saved_layers_size(-5) == 0
+    for batch in (1, 15, 16, 17, 65536, 70001, 1 << 31):
+        assert lib.fhoad_saved_layers_size(batch) == -(-batch // 16) * 49152, batch
+    assert lib.fhoad_saved_layers_size(65536) == 65536 * 3 * 64 * 4 * 4
 
 
 def test_torch_extension_reports_contract_errors_on_cpu() -> None:
@@ -208,6 +246,46 @@ def test_raw_entry_points_match_the_torch_extension() -> None:
         x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), gp.data_ptr(), gx.data_ptr(),
         ws.data_ptr(), ws_bytes - 1, batch, 6, stream)
     assert status == 4
+
+
+@pytest.mark.gpu
+def test_raw_saved_layer_pair_matches_the_pair() -> None:
+    """fhoad_forward_laplacian_saving and fhoad_forward_laplacian_backward_saved through ctypes
+    at 70,001 points (whole rounds plus split tiles): bitwise the outputs of
+    fhoad_forward_laplacian and the gradients of fhoad_forward_laplacian_backward."""
+    from gpu_helpers import announce, coordinates, packed, require_gpu_extension, upstream
+
+    require_gpu_extension()
+    announce("C ABI saved-layer pair via ctypes vs forward and backward, batch=70001")
+    from fused_hoad import _C
+
+    lib = _lib()
+    batch = 70001
+    p = packed(3)
+    x = coordinates(batch, seed=10)
+    gu, gl = upstream(batch, seed=10)
+    gu, gl = gu.reshape(-1).contiguous(), gl.reshape(-1).contiguous()
+    stream = torch.cuda.current_stream().cuda_stream
+    saved_bytes = lib.fhoad_saved_layers_size(batch)
+    saved = torch.empty(saved_bytes, dtype=torch.uint8, device="cuda")
+    u = torch.empty(batch, 1, device="cuda")
+    lap = torch.empty(batch, 1, device="cuda")
+    status = lib.fhoad_forward_laplacian_saving(x.data_ptr(), p.data_ptr(), u.data_ptr(), lap.data_ptr(),
+                                                saved.data_ptr(), saved_bytes, batch, 2, stream)
+    assert status == 0, lib.fhoad_last_error()
+    ws_bytes = lib.fhoad_backward_workspace_size(batch)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    gp = torch.empty(12737, device="cuda")
+    gx = torch.empty(batch, 2, device="cuda")
+    status = lib.fhoad_forward_laplacian_backward_saved(
+        x.data_ptr(), p.data_ptr(), saved.data_ptr(), saved_bytes, gu.data_ptr(), gl.data_ptr(),
+        gp.data_ptr(), gx.data_ptr(), ws.data_ptr(), ws_bytes, batch, 6, stream)
+    assert status == 0, lib.fhoad_last_error()
+    eu, el = _C.fused_forward_laplacian(x, p)
+    ep, ex = _C.fused_forward_laplacian_backward(x, p, gu, gl)
+    torch.cuda.synchronize()
+    assert torch.equal(u, eu) and torch.equal(lap, el)
+    assert torch.equal(gp, ep) and torch.equal(gx, ex)
 
 
 @pytest.mark.gpu

@@ -164,12 +164,14 @@ def test_graph_captured_training_step_matches_eager_step() -> None:
     torch.testing.assert_close(torch.tensor(train(True)), torch.tensor(train(False)), rtol=1e-4, atol=0)
 
 
-def test_graph_captured_flattened_step_matches_eager_at_64k() -> None:
-    """The drop-in step bench.py times as train_step_autograd_graphed_ms: a flattened model at
-    65,536 points (BASELINE config 3's size, where torch's mean reduces over many blocks),
-    captured whole and replayed 10 times with a host sync between replays, against the same
-    steps run eagerly: every replay's loss (rtol 1e-4) and the weights after."""
-    announce("whole-step graph capture vs eager, flattened model, batch=65536")
+@pytest.mark.parametrize("mode", ["cuda", "saved"])
+def test_graph_captured_flattened_step_matches_eager_at_64k(mode: str) -> None:
+    """The drop-in step bench.py times as train_step_autograd_graphed_ms (and, with
+    backward="saved", as ..._saved_ms): a flattened model at 65,536 points (BASELINE config 3's
+    size, where torch's mean reduces over many blocks), captured whole and replayed 10 times
+    with a host sync between replays, against the same steps run eagerly: every replay's loss
+    (rtol 1e-4) and the weights after."""
+    announce(f"whole-step graph capture vs eager, flattened model, batch=65536, backward={mode}")
     from fused_hoad import manufactured_source
     from fused_hoad.backends.fused import fused_laplacian
     from fused_hoad.parameters import flatten_poisson_parameters_
@@ -185,7 +187,7 @@ def test_graph_captured_flattened_step_matches_eager_at_64k() -> None:
 
     def loss_of(model):
         def loss_fn():
-            _, lap = fused_laplacian(model, x)
+            _, lap = fused_laplacian(model, x, backward=mode)
             return (lap - f).pow(2).mean()
         return loss_fn
 
