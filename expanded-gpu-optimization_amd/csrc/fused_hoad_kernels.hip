@@ -212,29 +212,66 @@ __device__ __forceinline__ void tanh_jet_adjoint_layer0(float v, float s, float 
   bl = bls;
 }
 
+// An opaque copy of a value: the compiler cannot see that it equals the input, so it cannot
+// hoist arithmetic on it (addresses, lane masks) out of the enclosing loop and keep the results
+// live, where at full register use they would be spilled; and a loaded value passed through it
+// is waited for there, not where the compiler would first use it.
+template <typename T>
+__device__ __forceinline__ T opaque(T x) {
+  __asm__ volatile("" : "+v"(x));
+  return x;
+}
+
 // Small-parameter staging shared by all kernels, in the scaled forms listed at kSmallCwx (the
-// factors 2 and 4 are exact).
-__device__ __forceinline__ void stage_small(const float* __restrict__ params, float* s_small,
-                                            int tid, int threads) {
-  for (int o = tid; o < kHidden; o += threads) {
-    const float wx = params[kInputs * o];
-    const float wy = params[kInputs * o + 1];
-    s_small[kSmallCwx + o] = kC * wx;
-    s_small[kSmallCwy + o] = kC * wy;
-    s_small[kSmallCb0 + o] = kC * params[kLayer0Bias + o];
-    s_small[kSmallWx + o] = 2.0f * wx;
-    s_small[kSmallWy + o] = 2.0f * wy;
-    s_small[kSmallQ0 + o] = 4.0f * __builtin_fmaf(wx, wx, wy * wy);
-    const float wo = params[kOutputBase + o];
-    s_small[kSmallWoutV + o] = 4.0f * (wo * (1.0f / kC));
-    s_small[kSmallWoutL + o] = 4.0f * (wo * (1.0f / kLambda));
+// factors 2 and 4 are exact), split into its global loads (load_small) and its LDS writes
+// (store_small), so that a kernel can issue these loads together with its other staging loads
+// and wait for global memory once: written as one function, each group of loads waited for the
+// previous group's LDS writes, and the forward's prologue made four round trips.
+// Thread tid < 64 holds neuron tid's W0 row, b0 and w_out, thread tid < 192 one hidden bias,
+// and every thread b_out (a uniform load).
+struct SmallLoads {
+  float wx, wy, b0, wo, bh, bout;
+};
+
+template <int kThreads>
+__device__ __forceinline__ SmallLoads load_small(const float* __restrict__ params, int tid) {
+  static_assert(kThreads >= 3 * kHidden, "one thread per hidden bias");
+  SmallLoads s{0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (tid < kHidden) {
+    s.wx = params[kInputs * tid];
+    s.wy = params[kInputs * tid + 1];
+    s.b0 = params[kLayer0Bias + tid];
+    s.wo = params[kOutputBase + tid];
   }
-  for (int k = tid; k < 3 * kHidden; k += threads) {
-    const int layer = k >> 6;
-    s_small[kSmallBh + k] =
-        kC * params[kHiddenBase + layer * kHiddenStride + kHidden * kHidden + (k & 63)];
+  if (tid < 3 * kHidden) {
+    s.bh = params[kHiddenBase + (tid >> 6) * kHiddenStride + kHidden * kHidden + (tid & 63)];
   }
-  if (tid == 0) s_small[kSmallBout] = params[kOutputBase + kHidden];
+  s.bout = params[kOutputBase + kHidden];
+  return s;
+}
+
+// Called after the caller's other staging loads are issued. The values are waited for here: the
+// opaque copies keep the compiler from moving the scaling up into load_small's branches, where
+// it would wait for the loads at once.
+__device__ __forceinline__ void store_small(float* s_small, int tid, SmallLoads s) {
+  s.wx = opaque(s.wx);
+  s.wy = opaque(s.wy);
+  s.b0 = opaque(s.b0);
+  s.wo = opaque(s.wo);
+  s.bh = opaque(s.bh);
+  s.bout = opaque(s.bout);
+  if (tid < kHidden) {
+    s_small[kSmallCwx + tid] = kC * s.wx;
+    s_small[kSmallCwy + tid] = kC * s.wy;
+    s_small[kSmallCb0 + tid] = kC * s.b0;
+    s_small[kSmallWx + tid] = 2.0f * s.wx;
+    s_small[kSmallWy + tid] = 2.0f * s.wy;
+    s_small[kSmallQ0 + tid] = 4.0f * __builtin_fmaf(s.wx, s.wx, s.wy * s.wy);
+    s_small[kSmallWoutV + tid] = 4.0f * (s.wo * (1.0f / kC));
+    s_small[kSmallWoutL + tid] = 4.0f * (s.wo * (1.0f / kLambda));
+  }
+  if (tid < 3 * kHidden) s_small[kSmallBh + tid] = kC * s.bh;
+  if (tid == 0) s_small[kSmallBout] = s.bout;
 }
 
 // Hidden-weight staging: every thread issues all of its global loads before its first LDS
@@ -278,10 +315,11 @@ __device__ __forceinline__ void stage_hidden(const float* __restrict__ params, i
 template <int kThreads>
 __device__ __forceinline__ void stage_parameters(const float* __restrict__ params, float* s_w,
                                                  float* s_small, int tid) {
+  const SmallLoads small = load_small<kThreads>(params, tid);
   stage_hidden<kThreads>(params, tid, [&](int layer, int o, int i, float value) {
     s_w[layer * kPlane + kWRow * o + i] = 4.0f * value;
   });
-  stage_small(params, s_small, tid, kThreads);
+  store_small(s_small, tid, small);
 }
 
 // Forward-only LDS layout of the hidden weights, in MFMA operand order: for hidden layer l,
@@ -292,30 +330,43 @@ __device__ __forceinline__ void stage_parameters(const float* __restrict__ param
 constexpr int kOperandLayerF4 = 16 * kWave;  // f4 entries per layer (16 KB)
 
 // Staging: work item (l, ob, lane) loads the 4 x 4 block of W_l with rows m, 16 + m, 32 + m,
-// 48 + m and columns 16 ob + 4 g .. + 3 (four 16-byte global loads, all issued before the
-// first LDS write) and stores its 4 columns as the 4 k-steps (ob, j) of that lane: 16-byte LDS
-// writes, each wave's 64 of them to 1 KB contiguous, so conflict-free. 768 work items: one per
-// thread of a 12-wave workgroup.
+// 48 + m and columns 16 ob + 4 g .. + 3 (four 16-byte global loads) and stores its 4 columns as
+// the 4 k-steps (ob, j) of that lane: 16-byte LDS writes, each wave's 64 of them to 1 KB
+// contiguous, so conflict-free. 768 work items: one per thread of a 12-wave workgroup, two for
+// some threads of an 8-wave one; a thread issues the loads of all its items before its first
+// LDS write.
 template <int kThreads>
 __device__ __forceinline__ void stage_operand_weights(const float* __restrict__ params, float* s_wa,
                                                       int tid) {
   constexpr int kItems = 3 * 4 * kWave;  // (layer, ob, lane)
+  constexpr int kPerThread = (kItems + kThreads - 1) / kThreads;
   const bool aligned = (reinterpret_cast<uintptr_t>(params) & 15) == 0;
   f4* wa = reinterpret_cast<f4*>(s_wa);
-  for (int item = tid; item < kItems; item += kThreads) {
-    const int lane = item & (kWave - 1), ob = (item >> 6) & 3, layer = item >> 8;
-    const float* block = params + kHiddenBase + layer * kHiddenStride + (lane & 15) * kHidden +
-                         16 * ob + 4 * (lane >> 4);
-    f4 rows[4];
+  f4 rows[kPerThread][4];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      const float* p = block + 16 * kHidden * mb;
-      rows[mb] = aligned ? *reinterpret_cast<const f4*>(p) : f4{p[0], p[1], p[2], p[3]};
+  for (int n = 0; n < kPerThread; ++n) {
+    const int item = tid + n * kThreads;
+    if (item < kItems) {
+      const int lane = item & (kWave - 1), ob = (item >> 6) & 3, layer = item >> 8;
+      const float* block = params + kHiddenBase + layer * kHiddenStride + (lane & 15) * kHidden +
+                           16 * ob + 4 * (lane >> 4);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const float* p = block + 16 * kHidden * mb;
+        rows[n][mb] = aligned ? *reinterpret_cast<const f4*>(p) : f4{p[0], p[1], p[2], p[3]};
+      }
     }
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      wa[(16 * layer + 4 * ob + j) * kWave + lane] =
-          4.0f * f4{rows[0][j], rows[1][j], rows[2][j], rows[3][j]};
+  for (int n = 0; n < kPerThread; ++n) {
+    const int item = tid + n * kThreads;
+    if (item < kItems) {
+      const int lane = item & (kWave - 1), ob = (item >> 6) & 3, layer = item >> 8;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        wa[(16 * layer + 4 * ob + j) * kWave + lane] =
+            4.0f * f4{rows[n][0][j], rows[n][1][j], rows[n][2][j], rows[n][3][j]};
+      }
     }
   }
 }
@@ -420,15 +471,6 @@ __device__ __forceinline__ void layer0_forward(const float* s_small, int g, floa
                                                f4 (&h)[4][4]) {
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) layer0_block(s_small, mb, g, x0, x1, h[mb]);
-}
-
-// An opaque copy of a value: the compiler cannot see that it equals the input, so it cannot
-// hoist arithmetic on it (addresses, lane masks) out of the enclosing loop and keep the results
-// live, where at full register use they would be spilled.
-template <typename T>
-__device__ __forceinline__ T opaque(T x) {
-  __asm__ volatile("" : "+v"(x));
-  return x;
 }
 
 // The small LDS parameters read per tile have loop-invariant addresses; left alone, the
@@ -620,8 +662,9 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
     next_x1 = coordinates[2 * (tile * kTile + m) + 1];
   }
   if (threadIdx.x == 0) s_quad = 0;
+  const SmallLoads small = load_small<kWaves * kWave>(params, threadIdx.x);
   stage_operand_weights<kWaves * kWave>(params, s_wa, threadIdx.x);
-  stage_small(params, s_small, threadIdx.x, kWaves * kWave);
+  store_small(s_small, threadIdx.x, small);
   __syncthreads();
   next_x0 = opaque(next_x0);  // delivered before the loop, for the same reason as below
   next_x1 = opaque(next_x1);
@@ -782,12 +825,14 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
                      int64_t tiles, f4* __restrict__ saved) {
   __shared__ f4 s_h[2][kSplitWaves][4][kWave];  // [buffer][wave][component][lane], 32 KB
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
-  stage_small(params, s_small, threadIdx.x, kSplitWaves * kWave);
-
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int m = lane & 15;
   const int g = lane >> 4;
+  // The small parameters are staged first and this wave's operands loaded after (they are needed
+  // only after the barrier and the first tile's coordinates): issued together, the operand loads
+  // were waited for before the barrier and a 1K-point call took 0.4 us longer.
+  store_small(s_small, threadIdx.x, load_small<kSplitWaves * kWave>(params, threadIdx.x));
   // A operands of this wave's rows: wa[l][ob][j] = 4 W_l[16 w + m][16 ob + 4 g + j] (the
   // scaled jet's weights), loaded once (global memory, L2-resident) instead of staging
   // the whole matrix in LDS.
@@ -1706,7 +1751,6 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ __attribute__((aligned(16))) float s_stage[kStageFloats];
   __shared__ float s_red[3][kBwdWaves];
-  if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] += 1.0f;
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int m = lane & 15;
@@ -1717,8 +1761,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     next = load_tile_inputs<kLoss, kRest>(coordinates, grad_output, grad_laplacian, batch, whole, seed,
                                    blockIdx.x, w, m);
   }
+  // kLoss: the Adam step count is read with the staging loads and advanced after the barrier
+  // (an increment in place waited for its load before wave 0 issued any staging load).
+  const float step_count = kLoss ? seed.step[0] : 0.0f;
   stage_parameters<kBwdWaves * kWave>(params, s_w, s_small, threadIdx.x);
   __syncthreads();
+  if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] = step_count + 1.0f;
 
   // Lane offsets into the LDS arrays. Each use forms its base from an opaque copy: the arrays
   // span more than the 64 KB reach of a DS offset, and hoisted bases would be spilled.
@@ -2045,14 +2093,23 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
   __shared__ f4 s_x[2][kSplitWaves][4][kWave];                       // lane-major exchange
   __shared__ __attribute__((aligned(16))) float s_zt[kSplitWaves][kTWave];
   __shared__ float s_gx[kSplitWaves][2][kTile];
-  if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] += 1.0f;
-  stage_parameters<kSplitWaves * kWave>(params, s_w, s_small, threadIdx.x);
-  __syncthreads();
-
   const int lane = threadIdx.x & (kWave - 1);
   const int w = threadIdx.x / kWave;
   const int m = lane & 15;
   const int g = lane >> 4;
+  // Per-point inputs of 16-point tiles (load_tile_inputs with no 64-point tiles): the first
+  // slot's first tile's are read before the staging and each next tile's during the current
+  // one, so no tile starts with a wait on global memory (a call here is a few tiles long).
+  TileInputs next{0.f, 0.f, 0.f, 0.f};
+  if (static_cast<int>(blockIdx.x) < slots) {
+    next = load_tile_inputs<kLoss, true>(coordinates, grad_output, grad_laplacian, batch, 0, seed,
+                                         blockIdx.x, w, m);
+  }
+  const float step_count = kLoss ? seed.step[0] : 0.0f;  // advanced below, as in backward_kernel
+  stage_parameters<kSplitWaves * kWave>(params, s_w, s_small, threadIdx.x);
+  __syncthreads();
+  if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] = step_count + 1.0f;
+
   const int rows_off = lane_rows(m, g) + 1088 * w;  // W[16 w + m][.] (forward operand)
   const int cols_off = lane_cols(m, g) + 16 * w;    // W[.][16 w + m] (transposed operand)
   const int t_read = m * kWRow + 4 * g;             // transposed reads: row m, points 4 s + g
@@ -2072,28 +2129,26 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
     float g_w0x = 0.f, g_w0y = 0.f, g_b0 = 0.f, g_wout = 0.f, g_bout = 0.f;
     float g_loss = 0.f, g_bloss = 0.f;
 
+    if (slot != static_cast<int>(blockIdx.x)) {
+      next = load_tile_inputs<kLoss, true>(coordinates, grad_output, grad_laplacian, batch, 0,
+                                           seed, slot, w, m);
+    }
     for (int64_t tile = slot; tile < tiles; tile += slots) {
       keep_lds_reads_in_loop();
+      const TileInputs in = next;
+      if (tile + slots < tiles) {
+        next = load_tile_inputs<kLoss, true>(coordinates, grad_output, grad_laplacian, batch, 0,
+                                             seed, tile + slots, w, m);
+      }
       const bool on_boundary = kLoss && tile >= seed.interior_tiles;  // uniform per workgroup
       const int64_t point = (on_boundary ? tile - seed.interior_tiles : tile) * kTile + m;
       const bool active = point < (on_boundary ? seed.boundary_count : batch);
-      const float* xy = on_boundary ? seed.boundary : coordinates;
-      float x0 = 0.f, x1 = 0.f, gu = 0.f, gl = 0.f, f = 0.f;
-      if (active) {
-        x0 = xy[2 * point];
-        x1 = xy[2 * point + 1];
-        if (kLoss) {
-          if (!on_boundary) f = seed.source[point];
-        } else {
-          gu = grad_output ? grad_output[point] : 0.0f;  // a null upstream gradient is zero
-          gl = grad_laplacian ? grad_laplacian[point] : 0.0f;
-        }
-      }
+      const float gu = kLoss ? 0.f : in.a, gl = kLoss ? 0.f : in.b, f = kLoss ? in.a : 0.f;
 
       SplitSums sums{g_w0x, g_w0y, g_b0, g_wout, g_bout, g_loss, g_bloss};
-      split_tile<kLoss>(s_w, s_small, scratch, phase, w, g, m, rows_off, cols_off, t_read, x0, x1,
-                        gu, gl, f, active, on_boundary, point, grad_coordinates, seed, dw, bias,
-                        sums);
+      split_tile<kLoss>(s_w, s_small, scratch, phase, w, g, m, rows_off, cols_off, t_read, in.x0,
+                        in.x1, gu, gl, f, active, on_boundary, point, grad_coordinates, seed, dw,
+                        bias, sums);
       g_w0x = sums.w0x;
       g_w0y = sums.w0y;
       g_b0 = sums.b0;
@@ -2101,6 +2156,7 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
       g_bout = sums.bout;
       g_loss = sums.loss;
       g_bloss = sums.bloss;
+      deliver(next);
     }
 
     // ---- this slot's partial row: each wave writes its own rows ----
