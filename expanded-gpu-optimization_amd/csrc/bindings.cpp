@@ -10,9 +10,11 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <c10/core/DeviceGuard.h>
 
+#include <array>
 #include <vector>
 
 #include "fused_hoad.h"
+#include "mlp_abi.h"
 
 namespace {
 
@@ -97,10 +99,6 @@ std::vector<torch::Tensor> fused_forward_laplacian_backward(torch::Tensor coordi
   return {grad_parameters, grad_coordinates};
 }
 
-// The backward for the autograd glue (no counterpart among the reference's bindings): either
-// upstream gradient may be None (zero, so no zeros tensor is made), and grad_coordinates is
-// computed only when want_coordinates is set (otherwise None is returned and nothing is
-// written). Same checks and kernels as fused_forward_laplacian_backward.
 // The forward of the autograd glue's "saved" mode: (u, Laplacian, saved layers), the last an
 // opaque uint8 buffer of fhoad_saved_layers_size(batch) bytes for backward_for_autograd.
 std::vector<torch::Tensor> forward_saving(torch::Tensor coordinates, torch::Tensor parameters,
@@ -124,8 +122,12 @@ std::vector<torch::Tensor> forward_saving(torch::Tensor coordinates, torch::Tens
   return {output, laplacian, saved};
 }
 
-// saved: forward_saving's buffer for the same coordinates and parameters (the backward then
-// reads the hidden layers instead of re-running the forward), or None.
+// The backward for the autograd glue (no counterpart among the reference's bindings): either
+// upstream gradient may be None (zero, so no zeros tensor is made), and grad_coordinates is
+// computed only when want_coordinates is set (otherwise None is returned and nothing is
+// written). Same checks and kernels as fused_forward_laplacian_backward. saved:
+// forward_saving's buffer for the same coordinates and parameters (the backward then reads the
+// hidden layers instead of re-running the forward), or None.
 std::vector<c10::optional<torch::Tensor>> backward_for_autograd(
     torch::Tensor coordinates, torch::Tensor parameters, c10::optional<torch::Tensor> grad_output,
     c10::optional<torch::Tensor> grad_laplacian, bool want_coordinates, int64_t version,
@@ -176,6 +178,107 @@ std::vector<c10::optional<torch::Tensor>> backward_for_autograd(
         static_cast<int>(version), current_stream(coordinates)));
   }
   return {grad_parameters, grad_coordinates};
+}
+
+// Where each of the model's ten parameters sits in the packed buffer (mlp_abi.h), in layout
+// order: weight then bias of each linear layer. cols == 0 marks a bias vector.
+struct PackedSlice {
+  int64_t offset, rows, cols;
+};
+constexpr int64_t hidden_base(int layer) { return fhoad::kHiddenBase + (layer - 1) * fhoad::kHiddenStride; }
+constexpr std::array<PackedSlice, 10> kPackedSlices{{
+    {0, fhoad::kHidden, fhoad::kInputs},
+    {fhoad::kLayer0Bias, fhoad::kHidden, 0},
+    {hidden_base(1), fhoad::kHidden, fhoad::kHidden},
+    {hidden_base(1) + fhoad::kHidden * fhoad::kHidden, fhoad::kHidden, 0},
+    {hidden_base(2), fhoad::kHidden, fhoad::kHidden},
+    {hidden_base(2) + fhoad::kHidden * fhoad::kHidden, fhoad::kHidden, 0},
+    {hidden_base(3), fhoad::kHidden, fhoad::kHidden},
+    {hidden_base(3) + fhoad::kHidden * fhoad::kHidden, fhoad::kHidden, 0},
+    {fhoad::kOutputBase, 1, fhoad::kHidden},
+    {fhoad::kOutputBase + fhoad::kHidden, 1, 0},
+}};
+static_assert(fhoad::kOutputBase + fhoad::kHidden + 1 == kParameterCount, "packed slices");
+
+// The autograd path of a model flattened onto one packed buffer (flatten_poisson_parameters_),
+// as a C++ autograd Function: the same forward, backward and gradients as the Python
+// FlattenedFusedLaplacian's "cuda*" and "saved" modes, without the Python Function's
+// per-step host work (its apply, the backward's Python frame and the ten gradient views built
+// in Python). Inputs: coordinates, the packed buffer, the forward and backward versions, whether
+// to keep the hidden layers for the backward ("saved"), and the ten parameters, which must be
+// the buffer's views in layout order; they are the Function's differentiable inputs, and each
+// gets a view of the packed gradient. An unused output's gradient arrives undefined and is read
+// as zero; the coordinate gradient is computed only when the coordinates need it.
+struct FlattenedLaplacian : public torch::autograd::Function<FlattenedLaplacian> {
+  static torch::autograd::variable_list forward(torch::autograd::AutogradContext* ctx,
+                                                const torch::Tensor& coordinates,
+                                                const torch::Tensor& flat, int64_t version,
+                                                int64_t backward_version, bool save_layers,
+                                                torch::TensorList parameters) {
+    TORCH_CHECK(backward_version >= 1 && backward_version <= 6, "backward version must be 1 to 6");
+    TORCH_CHECK(parameters.size() == kPackedSlices.size(), "expected the model's 10 parameters");
+    check_inputs(coordinates, flat);
+    const auto* base = static_cast<const char*>(flat.data_ptr());
+    for (size_t k = 0; k < kPackedSlices.size(); ++k) {
+      const PackedSlice& slice = kPackedSlices[k];
+      const torch::Tensor& p = parameters[k];
+      const bool shape_ok = slice.cols ? p.dim() == 2 && p.size(0) == slice.rows &&
+                                             p.size(1) == slice.cols && p.is_contiguous()
+                                       : p.dim() == 1 && p.size(0) == slice.rows;
+      TORCH_CHECK(shape_ok && static_cast<const char*>(p.data_ptr()) ==
+                                  base + sizeof(float) * slice.offset,
+                  "parameter ", k, " is not the packed buffer's view at its layout offset");
+    }
+    ctx->set_materialize_grads(false);
+    ctx->saved_data["backward_version"] = backward_version;
+    if (save_layers) {
+      std::vector<torch::Tensor> out = forward_saving(coordinates, flat, version);
+      ctx->save_for_backward({coordinates, flat, out[2]});
+      return {out[0], out[1]};
+    }
+    std::vector<torch::Tensor> out = fused_forward_laplacian(coordinates, flat, version);
+    ctx->save_for_backward({coordinates, flat});
+    return {out[0], out[1]};
+  }
+
+  static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
+                                                 torch::autograd::variable_list grads) {
+    // One gradient per forward argument: coordinates, flat, version, backward_version,
+    // save_layers, then the ten parameters (undefined where none).
+    torch::autograd::variable_list result(5 + kPackedSlices.size());
+    if (!grads[0].defined() && !grads[1].defined()) return result;
+    const auto saved = ctx->get_saved_variables();
+    const bool needs_coordinates = ctx->needs_input_grad(0);
+    bool needs_parameters = false;
+    for (size_t k = 0; k < kPackedSlices.size(); ++k) needs_parameters |= ctx->needs_input_grad(2 + k);
+    auto upstream = [](const torch::Tensor& g) -> c10::optional<torch::Tensor> {
+      if (!g.defined()) return c10::nullopt;
+      return g.reshape({-1}).contiguous();
+    };
+    const auto out = backward_for_autograd(
+        saved[0], saved[1], upstream(grads[0]), upstream(grads[1]), needs_coordinates,
+        ctx->saved_data["backward_version"].toInt(),
+        saved.size() > 2 ? c10::optional<torch::Tensor>(saved[2]) : c10::nullopt);
+    if (needs_coordinates) result[0] = *out[1];
+    if (needs_parameters) {
+      const torch::Tensor& grad_flat = *out[0];
+      for (size_t k = 0; k < kPackedSlices.size(); ++k) {
+        if (!ctx->needs_input_grad(2 + k)) continue;
+        const PackedSlice& slice = kPackedSlices[k];
+        result[5 + k] = slice.cols ? grad_flat.as_strided({slice.rows, slice.cols}, {slice.cols, 1}, slice.offset)
+                                   : grad_flat.as_strided({slice.rows}, {1}, slice.offset);
+      }
+    }
+    return result;
+  }
+};
+
+torch::autograd::variable_list flattened_laplacian(const torch::Tensor& coordinates,
+                                                   const torch::Tensor& flat, int64_t version,
+                                                   int64_t backward_version, bool save_layers,
+                                                   const std::vector<torch::Tensor>& parameters) {
+  return FlattenedLaplacian::apply(coordinates, flat, version, backward_version, save_layers,
+                                   torch::TensorList(parameters));
 }
 
 // One fused Poisson PINN + Adam training step (fhoad_poisson_adam_step). No counterpart among
@@ -255,6 +358,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
              pybind11::arg("grad_output"), pybind11::arg("grad_laplacian"),
              pybind11::arg("want_coordinates"), pybind11::arg("version") = 6,
              pybind11::arg("saved") = pybind11::none());
+  module.def("_flattened_laplacian", &flattened_laplacian,
+             "(u, Laplacian) of a flattened model through the C++ autograd Function",
+             pybind11::arg("coordinates"), pybind11::arg("flat"), pybind11::arg("version"),
+             pybind11::arg("backward_version"), pybind11::arg("save_layers"),
+             pybind11::arg("parameters"));
   module.def("_forward_saving", &forward_saving,
              "Forward that also keeps the hidden layers' outputs for _backward(saved=...)",
              pybind11::arg("coordinates"), pybind11::arg("parameters"),

@@ -23,7 +23,7 @@ from fused_hoad._extension import (
 from fused_hoad.backends.forward_laplacian import tanh_mlp_forward_laplacian
 from fused_hoad.parameters import (
     POISSON_PARAMETER_LAYOUT,
-    _linear_layers,
+    flattened_poisson_binding,
     flattened_poisson_parameters,
     pack_poisson_parameters,
     unpack_poisson_parameters,
@@ -94,55 +94,38 @@ class FusedForwardLaplacian(torch.autograd.Function):
 
 
 class FlattenedFusedLaplacian(torch.autograd.Function):
-    """``FusedForwardLaplacian`` for a model whose parameters are views of one packed buffer
-    (``flatten_poisson_parameters_``): the kernels read that buffer directly, the autograd
-    inputs are the model's ten parameters themselves, and the backward hands each one a view
-    of the packed gradient. A training step then has no ``torch.cat`` pack, no cat backward
-    and no per-parameter gradient copies. An output the loss does not use reaches the
-    backward as ``None``, which the kernel reads as zero (no zeros tensor is made), and the
-    coordinate gradient is computed only when the coordinates require it."""
+    """The ``"recompute"`` mode for a model whose parameters are views of one packed buffer
+    (``flatten_poisson_parameters_``): the kernel reads that buffer directly, the autograd
+    inputs are the model's ten parameters themselves, and the backward (the PyTorch reference
+    backward) hands each one a view of the packed gradient. The ``"cuda*"`` and ``"saved"``
+    modes of this path run the C++ autograd Function behind ``_C._flattened_laplacian``, which
+    does the same without the Python Function's per-step host work. An output the loss does
+    not use reaches the backward as ``None`` and is read as zero."""
 
     @staticmethod
-    def forward(ctx, coordinates: Tensor, flat: Tensor, version: int, backward: str, *parameters: Tensor):
-        ctx.backward_mode = backward
+    def forward(ctx, coordinates: Tensor, flat: Tensor, version: int, *parameters: Tensor):
         ctx.set_materialize_grads(False)
-        if backward == SAVED_MODE:
-            output, laplacian, saved = load_extension()._forward_saving(coordinates, flat, version)
-            ctx.save_for_backward(coordinates, flat, saved)
-            return output, laplacian
         ctx.save_for_backward(coordinates, flat)
         return fused_forward_laplacian(coordinates, flat, version)
 
     @staticmethod
     def backward(ctx, grad_output: Tensor | None, grad_laplacian: Tensor | None):
-        coordinates, flat, *saved = ctx.saved_tensors
+        coordinates, flat = ctx.saved_tensors
         needs_coordinates = ctx.needs_input_grad[0]
-        needs_parameters = any(ctx.needs_input_grad[4:])
+        needs_parameters = any(ctx.needs_input_grad[3:])
         if grad_output is None and grad_laplacian is None:
-            return (None,) * (4 + len(POISSON_PARAMETER_LAYOUT) * 2)
-        mode = ctx.backward_mode
-        if mode in _CUDA_BACKWARD_VERSIONS or mode == SAVED_MODE:
-            grad_flat, grad_coordinates = load_extension()._backward(
-                coordinates,
-                flat,
-                None if grad_output is None else grad_output.reshape(-1).contiguous(),
-                None if grad_laplacian is None else grad_laplacian.reshape(-1).contiguous(),
-                needs_coordinates,
-                _CUDA_BACKWARD_VERSIONS.get(mode, 6),
-                saved[0] if saved else None,
-            )
-        else:
-            zeros = torch.zeros(coordinates.shape[0], 1, dtype=flat.dtype, device=flat.device)
-            grad_coordinates, grad_flat = _recompute_backward(
-                coordinates,
-                flat,
-                zeros if grad_output is None else grad_output,
-                zeros if grad_laplacian is None else grad_laplacian,
-                needs_coordinates,
-                True,
-            )
+            return (None,) * (3 + len(POISSON_PARAMETER_LAYOUT) * 2)
+        zeros = torch.zeros(coordinates.shape[0], 1, dtype=flat.dtype, device=flat.device)
+        grad_coordinates, grad_flat = _recompute_backward(
+            coordinates,
+            flat,
+            zeros if grad_output is None else grad_output,
+            zeros if grad_laplacian is None else grad_laplacian,
+            needs_coordinates,
+            True,
+        )
         grads: list[Tensor | None] = []
-        for spec, needs in zip(POISSON_PARAMETER_LAYOUT, _pairs(ctx.needs_input_grad[4:]), strict=True):
+        for spec, needs in zip(POISSON_PARAMETER_LAYOUT, _pairs(ctx.needs_input_grad[3:]), strict=True):
             grads.append(
                 grad_flat[spec.weight_offset : spec.bias_offset].view(spec.out_features, spec.in_features)
                 if needs[0] else None
@@ -150,16 +133,11 @@ class FlattenedFusedLaplacian(torch.autograd.Function):
             grads.append(grad_flat[spec.bias_offset : spec.end_offset] if needs[1] else None)
         if not needs_parameters:
             grads = [None] * len(grads)
-        return (grad_coordinates if needs_coordinates else None, None, None, None, *grads)
+        return (grad_coordinates if needs_coordinates else None, None, None, *grads)
 
 
 def _pairs(flags):
     return [(flags[i], flags[i + 1]) for i in range(0, len(flags), 2)]
-
-
-def _flattened_parameter_list(model: nn.Module) -> list[Tensor]:
-    """The model's weights and biases in packed-layout order."""
-    return [t for layer in _linear_layers(model) for t in (layer.weight, layer.bias)]
 
 
 def _recompute_backward(
@@ -225,12 +203,19 @@ def fused_laplacian(
     if backward not in _ACCEPTED_MODES:
         raise ValueError(f"backward must be one of {_ACCEPTED_MODES}")
     if torch.is_grad_enabled():
-        flat = flattened_poisson_parameters(model)
-        if flat is not None:  # parameters are views of the packed buffer: no pack at all
-            tensors = _flattened_parameter_list(model)
+        binding = flattened_poisson_binding(model)
+        if binding is not None:  # parameters are views of the packed buffer: no pack at all
+            flat, tensors = binding
+            coordinates = coordinates.contiguous()
             if coordinates.requires_grad or any(t.requires_grad for t in tensors):
-                return FlattenedFusedLaplacian.apply(coordinates.contiguous(), flat, version, backward, *tensors)
-            return fused_forward_laplacian(coordinates.contiguous(), flat, version)
+                if backward == "recompute":
+                    return FlattenedFusedLaplacian.apply(coordinates, flat, version, *tensors)
+                u, lap = load_extension()._flattened_laplacian(
+                    coordinates, flat, version, _CUDA_BACKWARD_VERSIONS.get(backward, 6),
+                    backward == SAVED_MODE, tensors,
+                )
+                return u, lap
+            return fused_forward_laplacian(coordinates, flat, version)
     parameters = _packed_parameters(model)
     if parameters.requires_grad or coordinates.requires_grad:
         return FusedForwardLaplacian.apply(coordinates.contiguous(), parameters, version, backward)

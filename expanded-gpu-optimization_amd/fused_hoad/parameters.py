@@ -128,16 +128,28 @@ def flatten_poisson_parameters_(model: nn.Module) -> Tensor:
 def flattened_poisson_parameters(model: nn.Module) -> Tensor | None:
     """The packed buffer the model's parameters are views of, or ``None`` if they are not
     (never flattened, moved, or a parameter reassigned since)."""
+    binding = flattened_poisson_binding(model)
+    return None if binding is None else binding[0]
+
+
+def flattened_poisson_binding(model: nn.Module) -> tuple[Tensor, list[Tensor]] | None:
+    """``(packed buffer, the ten parameters in layout order)`` for a model whose parameters are
+    views of the buffer at their layout offsets, else ``None``; one walk over the modules (the
+    autograd path calls it every step)."""
     flat = getattr(model, "_fused_hoad_packed", None)
     if flat is None:
         return None
     base = flat.data_ptr()
     item = flat.element_size()
+    tensors: list[Tensor] = []
     for layer, spec in zip(_linear_layers(model), POISSON_PARAMETER_LAYOUT, strict=True):
+        weight, bias = layer.weight, layer.bias
         if (
-            layer.weight.data_ptr() != base + item * spec.weight_offset
-            or layer.bias.data_ptr() != base + item * spec.bias_offset
-            or layer.weight.device != flat.device
+            weight.data_ptr() != base + item * spec.weight_offset
+            or bias.data_ptr() != base + item * spec.bias_offset
         ):
             return None
-    return flat
+        tensors += (weight, bias)
+    if tensors[0].device != flat.device:
+        return None
+    return flat, tensors

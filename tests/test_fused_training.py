@@ -100,6 +100,65 @@ def test_flattened_model_gradients_equal_the_packed_path(loss_kind: str, coordin
         assert torch.equal(got_x, want_x)
 
 
+@pytest.mark.parametrize("mode", ["cuda", "saved", "recompute"])
+def test_flattened_model_with_frozen_layers(mode: str) -> None:
+    """Layers 0 and 4 frozen (requires_grad False) on a flattened model: they get no gradient,
+    and the trainable layers' gradients and the coordinate gradient are bitwise those of an
+    unflattened twin frozen the same way."""
+    announce(f"flattened model with frozen layers 0 and 4, backward={mode}")
+    from fused_hoad import manufactured_source
+    from fused_hoad.backends.fused import fused_laplacian
+    from fused_hoad.parameters import flatten_poisson_parameters_
+
+    x0 = coordinates(3000, seed=32)
+    f = manufactured_source(x0)
+
+    def run(flatten: bool):
+        model = _model(6)
+        if flatten:
+            flatten_poisson_parameters_(model)
+        frozen = [model[0], model[-1]]
+        for layer in frozen:
+            layer.weight.requires_grad_(False)
+            layer.bias.requires_grad_(False)
+        x = x0.clone().requires_grad_(True)
+        u, lap = fused_laplacian(model, x, backward=mode)
+        ((lap - f).pow(2).mean() + 0.1 * u.pow(2).mean()).backward()
+        return [p.grad for p in model.parameters()], x.grad
+
+    want, want_x = run(False)
+    got, got_x = run(True)
+    torch.cuda.synchronize()
+    for index, (a, b) in enumerate(zip(got, want, strict=True)):
+        if index in (0, 1, 8, 9):
+            assert a is None and b is None, index
+        else:
+            assert torch.equal(a, b), f"parameter {index}"
+    assert torch.equal(got_x, want_x)
+
+
+def test_flattened_function_rejects_parameters_that_are_not_the_buffer_views() -> None:
+    announce("C++ flattened autograd Function: parameter geometry check")
+    from fused_hoad import _C
+    from fused_hoad.parameters import flatten_poisson_parameters_, flattened_poisson_binding
+
+    model = _model(7)
+    flatten_poisson_parameters_(model)
+    flat, tensors = flattened_poisson_binding(model)
+    x = coordinates(100, seed=33)
+    swapped = [tensors[2], *tensors[1:2], tensors[0], *tensors[3:]]
+    with pytest.raises(RuntimeError, match="is not the packed buffer's view"):
+        _C._flattened_laplacian(x, flat, 2, 6, False, swapped)
+    with pytest.raises(RuntimeError, match="expected the model's 10 parameters"):
+        _C._flattened_laplacian(x, flat, 2, 6, False, tensors[:9])
+    u, lap = _C._flattened_laplacian(x, flat, 2, 6, False, tensors)
+    from fused_hoad import fused_forward_laplacian
+
+    ref_u, ref_lap = fused_forward_laplacian(x, flat, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(u, ref_u) and torch.equal(lap, ref_lap)
+
+
 def test_fused_trains_like_forward_laplacian() -> None:
     announce("50 Adam steps, fused vs forward_laplacian, batch=2048")
     from fused_hoad import forward_laplacian, get_backend
