@@ -200,37 +200,54 @@ constexpr std::array<PackedSlice, 10> kPackedSlices{{
 }};
 static_assert(fhoad::kOutputBase + fhoad::kHidden + 1 == kParameterCount, "packed slices");
 
-// The autograd path of a model flattened onto one packed buffer (flatten_poisson_parameters_),
-// as a C++ autograd Function: the same forward, backward and gradients as the Python
-// FlattenedFusedLaplacian's "cuda*" and "saved" modes, without the Python Function's
-// per-step host work (its apply, the backward's Python frame and the ten gradient views built
-// in Python). Inputs: coordinates, the packed buffer, the forward and backward versions, whether
-// to keep the hidden layers for the backward ("saved"), and the ten parameters, which must be
-// the buffer's views in layout order; they are the Function's differentiable inputs, and each
-// gets a view of the packed gradient. An unused output's gradient arrives undefined and is read
-// as zero; the coordinate gradient is computed only when the coordinates need it.
-struct FlattenedLaplacian : public torch::autograd::Function<FlattenedLaplacian> {
+// The autograd path of fused_laplacian's "cuda*" and "saved" modes as a C++ autograd Function:
+// the same forward, backward and gradients as the Python Functions of fused.py, without their
+// per-step host work (the Python apply, the backward's Python frame, the differentiable
+// torch.cat pack and its backward, or the ten gradient views built in Python). Inputs:
+// coordinates; the packed buffer when the model's parameters are its views
+// (flatten_poisson_parameters_), else None; the forward and backward versions; whether to keep
+// the hidden layers for the backward ("saved"); and the ten parameters in layout order (weight
+// then bias of each linear layer), the Function's differentiable inputs. Without a buffer the
+// parameters are packed into a new one (one copy kernel, outside autograd). Each parameter gets
+// a view of the packed gradient with its own shape. An unused output's gradient arrives
+// undefined and is read as zero; the coordinate gradient is computed only when the coordinates
+// need it.
+struct ModelLaplacian : public torch::autograd::Function<ModelLaplacian> {
   static torch::autograd::variable_list forward(torch::autograd::AutogradContext* ctx,
                                                 const torch::Tensor& coordinates,
-                                                const torch::Tensor& flat, int64_t version,
-                                                int64_t backward_version, bool save_layers,
-                                                torch::TensorList parameters) {
+                                                const c10::optional<torch::Tensor>& packed,
+                                                int64_t version, int64_t backward_version,
+                                                bool save_layers, torch::TensorList parameters) {
     TORCH_CHECK(backward_version >= 1 && backward_version <= 6, "backward version must be 1 to 6");
     TORCH_CHECK(parameters.size() == kPackedSlices.size(), "expected the model's 10 parameters");
-    check_inputs(coordinates, flat);
-    const auto* base = static_cast<const char*>(flat.data_ptr());
     for (size_t k = 0; k < kPackedSlices.size(); ++k) {
       const PackedSlice& slice = kPackedSlices[k];
       const torch::Tensor& p = parameters[k];
-      const bool shape_ok = slice.cols ? p.dim() == 2 && p.size(0) == slice.rows &&
-                                             p.size(1) == slice.cols && p.is_contiguous()
+      const bool shape_ok = slice.cols ? p.dim() == 2 && p.size(0) == slice.rows && p.size(1) == slice.cols
                                        : p.dim() == 1 && p.size(0) == slice.rows;
-      TORCH_CHECK(shape_ok && static_cast<const char*>(p.data_ptr()) ==
-                                  base + sizeof(float) * slice.offset,
-                  "parameter ", k, " is not the packed buffer's view at its layout offset");
+      TORCH_CHECK(shape_ok, "parameter ", k, " must have the shape of layout slice ", k);
+    }
+    torch::Tensor flat;
+    if (packed.has_value()) {
+      flat = *packed;
+      check_inputs(coordinates, flat);
+      const auto* base = static_cast<const char*>(flat.data_ptr());
+      for (size_t k = 0; k < kPackedSlices.size(); ++k) {
+        const torch::Tensor& p = parameters[k];
+        TORCH_CHECK(p.is_contiguous() && static_cast<const char*>(p.data_ptr()) ==
+                                             base + sizeof(float) * kPackedSlices[k].offset,
+                    "parameter ", k, " is not the packed buffer's view at its layout offset");
+      }
+    } else {
+      std::vector<torch::Tensor> pieces;
+      pieces.reserve(parameters.size());
+      for (const torch::Tensor& p : parameters) pieces.push_back(p.reshape({-1}));
+      flat = torch::cat(pieces);
+      check_inputs(coordinates, flat);
     }
     ctx->set_materialize_grads(false);
     ctx->saved_data["backward_version"] = backward_version;
+    ctx->saved_data["packed_given"] = packed.has_value();
     if (save_layers) {
       std::vector<torch::Tensor> out = forward_saving(coordinates, flat, version);
       ctx->save_for_backward({coordinates, flat, out[2]});
@@ -243,14 +260,18 @@ struct FlattenedLaplacian : public torch::autograd::Function<FlattenedLaplacian>
 
   static torch::autograd::variable_list backward(torch::autograd::AutogradContext* ctx,
                                                  torch::autograd::variable_list grads) {
-    // One gradient per forward argument: coordinates, flat, version, backward_version,
-    // save_layers, then the ten parameters (undefined where none).
+    // One gradient per forward argument: coordinates, packed, version, backward_version,
+    // save_layers, then the ten parameters (undefined where none). The differentiable inputs
+    // are the coordinates (input 0), the packed buffer when given, and the parameters.
     torch::autograd::variable_list result(5 + kPackedSlices.size());
     if (!grads[0].defined() && !grads[1].defined()) return result;
     const auto saved = ctx->get_saved_variables();
+    const size_t first_parameter = ctx->saved_data["packed_given"].toBool() ? 2 : 1;
     const bool needs_coordinates = ctx->needs_input_grad(0);
     bool needs_parameters = false;
-    for (size_t k = 0; k < kPackedSlices.size(); ++k) needs_parameters |= ctx->needs_input_grad(2 + k);
+    for (size_t k = 0; k < kPackedSlices.size(); ++k) {
+      needs_parameters |= ctx->needs_input_grad(first_parameter + k);
+    }
     auto upstream = [](const torch::Tensor& g) -> c10::optional<torch::Tensor> {
       if (!g.defined()) return c10::nullopt;
       return g.reshape({-1}).contiguous();
@@ -263,7 +284,7 @@ struct FlattenedLaplacian : public torch::autograd::Function<FlattenedLaplacian>
     if (needs_parameters) {
       const torch::Tensor& grad_flat = *out[0];
       for (size_t k = 0; k < kPackedSlices.size(); ++k) {
-        if (!ctx->needs_input_grad(2 + k)) continue;
+        if (!ctx->needs_input_grad(first_parameter + k)) continue;
         const PackedSlice& slice = kPackedSlices[k];
         result[5 + k] = slice.cols ? grad_flat.as_strided({slice.rows, slice.cols}, {slice.cols, 1}, slice.offset)
                                    : grad_flat.as_strided({slice.rows}, {1}, slice.offset);
@@ -273,12 +294,13 @@ struct FlattenedLaplacian : public torch::autograd::Function<FlattenedLaplacian>
   }
 };
 
-torch::autograd::variable_list flattened_laplacian(const torch::Tensor& coordinates,
-                                                   const torch::Tensor& flat, int64_t version,
-                                                   int64_t backward_version, bool save_layers,
-                                                   const std::vector<torch::Tensor>& parameters) {
-  return FlattenedLaplacian::apply(coordinates, flat, version, backward_version, save_layers,
-                                   torch::TensorList(parameters));
+torch::autograd::variable_list model_laplacian(const torch::Tensor& coordinates,
+                                               const c10::optional<torch::Tensor>& packed,
+                                               int64_t version, int64_t backward_version,
+                                               bool save_layers,
+                                               const std::vector<torch::Tensor>& parameters) {
+  return ModelLaplacian::apply(coordinates, packed, version, backward_version, save_layers,
+                               torch::TensorList(parameters));
 }
 
 // One fused Poisson PINN + Adam training step (fhoad_poisson_adam_step). No counterpart among
@@ -358,9 +380,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
              pybind11::arg("grad_output"), pybind11::arg("grad_laplacian"),
              pybind11::arg("want_coordinates"), pybind11::arg("version") = 6,
              pybind11::arg("saved") = pybind11::none());
-  module.def("_flattened_laplacian", &flattened_laplacian,
-             "(u, Laplacian) of a flattened model through the C++ autograd Function",
-             pybind11::arg("coordinates"), pybind11::arg("flat"), pybind11::arg("version"),
+  module.def("_model_laplacian", &model_laplacian,
+             "(u, Laplacian) of the model's ten parameters through the C++ autograd Function",
+             pybind11::arg("coordinates"), pybind11::arg("packed"), pybind11::arg("version"),
              pybind11::arg("backward_version"), pybind11::arg("save_layers"),
              pybind11::arg("parameters"));
   module.def("_forward_saving", &forward_saving,

@@ -26,6 +26,7 @@ from fused_hoad.parameters import (
     flattened_poisson_binding,
     flattened_poisson_parameters,
     pack_poisson_parameters,
+    poisson_parameter_tensors,
     unpack_poisson_parameters,
 )
 
@@ -98,8 +99,8 @@ class FlattenedFusedLaplacian(torch.autograd.Function):
     (``flatten_poisson_parameters_``): the kernel reads that buffer directly, the autograd
     inputs are the model's ten parameters themselves, and the backward (the PyTorch reference
     backward) hands each one a view of the packed gradient. The ``"cuda*"`` and ``"saved"``
-    modes of this path run the C++ autograd Function behind ``_C._flattened_laplacian``, which
-    does the same without the Python Function's per-step host work. An output the loss does
+    modes run the C++ autograd Function behind ``_C._model_laplacian``, which does the same
+    without the Python Function's per-step host work. An output the loss does
     not use reaches the backward as ``None`` and is read as zero."""
 
     @staticmethod
@@ -203,18 +204,20 @@ def fused_laplacian(
     if backward not in _ACCEPTED_MODES:
         raise ValueError(f"backward must be one of {_ACCEPTED_MODES}")
     if torch.is_grad_enabled():
+        # A flattened model's parameters are views of its packed buffer: no pack at all.
         binding = flattened_poisson_binding(model)
-        if binding is not None:  # parameters are views of the packed buffer: no pack at all
-            flat, tensors = binding
-            coordinates = coordinates.contiguous()
-            if coordinates.requires_grad or any(t.requires_grad for t in tensors):
-                if backward == "recompute":
-                    return FlattenedFusedLaplacian.apply(coordinates, flat, version, *tensors)
-                u, lap = load_extension()._flattened_laplacian(
+        flat, tensors = binding if binding is not None else (None, poisson_parameter_tensors(model))
+        coordinates = coordinates.contiguous()
+        if coordinates.requires_grad or any(t.requires_grad for t in tensors):
+            if backward != "recompute":
+                u, lap = load_extension()._model_laplacian(
                     coordinates, flat, version, _CUDA_BACKWARD_VERSIONS.get(backward, 6),
                     backward == SAVED_MODE, tensors,
                 )
                 return u, lap
+            if flat is not None:
+                return FlattenedFusedLaplacian.apply(coordinates, flat, version, *tensors)
+        elif flat is not None:
             return fused_forward_laplacian(coordinates, flat, version)
     parameters = _packed_parameters(model)
     if parameters.requires_grad or coordinates.requires_grad:

@@ -59,11 +59,13 @@ def _linear_layers(model: nn.Module) -> list[nn.Linear]:
     return [module for module in model.modules() if isinstance(module, nn.Linear)]
 
 
-def _segments(model: nn.Module) -> list[Tensor]:
+def poisson_parameter_tensors(model: nn.Module) -> list[Tensor]:
+    """The model's ten weights and biases in packed-layout order, checked against the layout
+    (the pack's errors and messages)."""
     layers = _linear_layers(model)
     if len(layers) != len(POISSON_PARAMETER_LAYOUT):
         raise ValueError(f"expected {len(POISSON_PARAMETER_LAYOUT)} linear layers")
-    segments: list[Tensor] = []
+    tensors: list[Tensor] = []
     for layer, spec in zip(layers, POISSON_PARAMETER_LAYOUT, strict=True):
         expected = (spec.out_features, spec.in_features)
         if tuple(layer.weight.shape) != expected:
@@ -72,8 +74,12 @@ def _segments(model: nn.Module) -> list[Tensor]:
             )
         if layer.bias is None or tuple(layer.bias.shape) != (spec.out_features,):
             raise ValueError(f"{spec.name}.bias must have shape ({spec.out_features},)")
-        segments += [layer.weight.reshape(-1), layer.bias.reshape(-1)]
-    return segments
+        tensors += (layer.weight, layer.bias)
+    return tensors
+
+
+def _segments(model: nn.Module) -> list[Tensor]:
+    return [tensor.reshape(-1) for tensor in poisson_parameter_tensors(model)]
 
 
 def pack_poisson_parameters(model: nn.Module, *, differentiable: bool = False) -> Tensor:

@@ -64,8 +64,9 @@ def test_flattened_model_gradients_equal_the_packed_path(loss_kind: str, coordin
     """A model flattened with flatten_poisson_parameters_ takes the no-pack autograd path
     (its parameters are the Function's inputs, their gradients views of the packed one, an
     unused output's gradient is read as zero without a zeros tensor, the coordinate gradient is
-    skipped unless needed). Its gradients are bitwise those of the torch.cat path of an
-    unflattened twin, which passes materialized zeros and always computes grad_coordinates."""
+    skipped unless needed). Its gradients are bitwise those of an unflattened twin, whose
+    parameters are packed on every call (by the C++ Function, or by the differentiable
+    torch.cat of the recompute mode)."""
     announce(f"flattened vs packed autograd path, loss={loss_kind}, coordinate grad={coordinate_grad}, backward={mode}")
     from fused_hoad import manufactured_source
     from fused_hoad.backends.fused import fused_laplacian
@@ -137,26 +138,59 @@ def test_flattened_model_with_frozen_layers(mode: str) -> None:
     assert torch.equal(got_x, want_x)
 
 
-def test_flattened_function_rejects_parameters_that_are_not_the_buffer_views() -> None:
-    announce("C++ flattened autograd Function: parameter geometry check")
-    from fused_hoad import _C
+def test_model_laplacian_function_checks_its_parameters() -> None:
+    """The C++ autograd Function behind fused_laplacian: the parameters must have the layout's
+    shapes and, with a packed buffer given, be its views; without one it packs them itself."""
+    announce("C++ autograd Function: parameter checks, packed and unpacked forms")
+    from fused_hoad import _C, fused_forward_laplacian, pack_poisson_parameters
     from fused_hoad.parameters import flatten_poisson_parameters_, flattened_poisson_binding
 
     model = _model(7)
     flatten_poisson_parameters_(model)
     flat, tensors = flattened_poisson_binding(model)
     x = coordinates(100, seed=33)
-    swapped = [tensors[2], *tensors[1:2], tensors[0], *tensors[3:]]
-    with pytest.raises(RuntimeError, match="is not the packed buffer's view"):
-        _C._flattened_laplacian(x, flat, 2, 6, False, swapped)
+    with pytest.raises(RuntimeError, match="must have the shape of layout slice 0"):
+        _C._model_laplacian(x, flat, 2, 6, False, [tensors[2], *tensors[1:]])
+    with pytest.raises(RuntimeError, match="parameter 3 is not the packed buffer's view"):
+        _C._model_laplacian(x, flat, 2, 6, False, [*tensors[:3], tensors[3].clone(), *tensors[4:]])
     with pytest.raises(RuntimeError, match="expected the model's 10 parameters"):
-        _C._flattened_laplacian(x, flat, 2, 6, False, tensors[:9])
-    u, lap = _C._flattened_laplacian(x, flat, 2, 6, False, tensors)
-    from fused_hoad import fused_forward_laplacian
-
+        _C._model_laplacian(x, flat, 2, 6, False, tensors[:9])
+    u, lap = _C._model_laplacian(x, flat, 2, 6, False, tensors)
     ref_u, ref_lap = fused_forward_laplacian(x, flat, 2)
+    twin = _model(7)
+    packed_u, packed_lap = _C._model_laplacian(x, None, 2, 6, False, list(twin.parameters()))
     torch.cuda.synchronize()
+    assert torch.equal(pack_poisson_parameters(twin), flat)
     assert torch.equal(u, ref_u) and torch.equal(lap, ref_lap)
+    assert torch.equal(packed_u, ref_u) and torch.equal(packed_lap, ref_lap)
+
+
+@pytest.mark.parametrize("mode", ["cuda", "saved", "recompute"])
+def test_public_python_function_equals_fused_laplacian(mode: str) -> None:
+    """FusedForwardLaplacian, the reference's public autograd Function over a packed buffer,
+    called directly on a differentiable pack: the same u, Laplacian and gradients, bitwise, as
+    fused_laplacian (whose "cuda" and "saved" modes run the C++ Function)."""
+    announce(f"FusedForwardLaplacian.apply vs fused_laplacian, backward={mode}")
+    from fused_hoad import manufactured_source, pack_poisson_parameters
+    from fused_hoad.backends.fused import FusedForwardLaplacian, fused_laplacian
+
+    x0 = coordinates(2500, seed=34)
+    f = manufactured_source(x0)
+
+    def run(direct: bool):
+        model = _model(8)
+        x = x0.clone().requires_grad_(True)
+        if direct:
+            u, lap = FusedForwardLaplacian.apply(x, pack_poisson_parameters(model, differentiable=True), 2, mode)
+        else:
+            u, lap = fused_laplacian(model, x, backward=mode)
+        ((lap - f).pow(2).mean() + 0.1 * u.pow(2).mean()).backward()
+        return [u.detach(), lap.detach(), x.grad] + [p.grad for p in model.parameters()]
+
+    want, got = run(False), run(True)
+    torch.cuda.synchronize()
+    for index, (a, b) in enumerate(zip(got, want, strict=True)):
+        assert torch.equal(a, b), index
 
 
 def test_fused_trains_like_forward_laplacian() -> None:
