@@ -2309,9 +2309,11 @@ __global__ void fill_zero_kernel(float* __restrict__ out, int64_t n) {
 // ---------------------------------------------------------------------------------------------
 // Host side.
 
-// Forward workgroup: 12 waves, 3 per SIMD (150 VGPRs each). Measured against 8 waves: 3 % faster
-// at 64K points, 5 % at 256K; a CU's 16 tiles per 64K still split 4 per SIMD.
+// Forward workgroup: 12 waves, 3 per SIMD (152 VGPRs each), about 1 % faster than 8 waves at 64K
+// and 256K points; a CU's 16 tiles per 64K still split 4 per SIMD. The saving forward runs 8
+// (launch_forward).
 constexpr int kFwdWaves = 12;
+constexpr int kSaveFwdWaves = 8;
 constexpr int kSplitTilesPerCu = 2;  // forward_split_kernel up to this many tiles per CU
 
 thread_local char g_last_error[512] = "";
@@ -2529,9 +2531,15 @@ int launch_forward(const float* coordinates, const float* parameters, float* out
     return check_launch("forward_split_kernel");
   }
   const int64_t whole = forward_whole_tiles(tiles, grid);
-  // FUSED_HOAD_FWD_WAVES=8 (experiment knob, read per call) selects 8 waves per workgroup.
-  const char* env = std::getenv("FUSED_HOAD_FWD_WAVES");
-  if (env && std::atoi(env) == 8) {
+  // Waves per workgroup: 12 for the forward; 8 for the saving forward, whose 48 KB of stores per
+  // tile slowed the 12-wave form more (64K points: 69 against 60 us; the plain forward 51.1
+  // against 51.6 us). FUSED_HOAD_FWD_WAVES=8 / 12 (experiment knob, read per call) forces either.
+  int waves = kSave ? kSaveFwdWaves : kFwdWaves;
+  if (const char* env = std::getenv("FUSED_HOAD_FWD_WAVES")) {
+    const int forced = std::atoi(env);
+    if (forced == 8 || forced == 12) waves = forced;
+  }
+  if (waves == 8) {
     hipLaunchKernelGGL((forward_kernel<8, kSave>), dim3(grid), dim3(8 * kWave), 0, hs, coordinates,
                        parameters, output, laplacian, batch, whole, tiles, saved_f4);
   } else {

@@ -33,16 +33,18 @@ def _saving_forward(x, p):
 
 @pytest.mark.parametrize(
     "batch,waves",
-    [(1, "12"), (17, "12"), (1000, "12"), (8192, "12"), (16401, "12"), (65536, "12"),
-     (65537, "12"), (70000, "12"), (70000, "8"), (262145, "12")],
+    [(1, None), (17, None), (1000, None), (8192, None), (16401, None), (65536, None),
+     (65537, None), (70000, None), (262145, None), (65536, "12"), (70000, "12"), (70000, "8")],
 )
-def test_saving_forward_is_bitwise_the_forward(batch: int, waves: str) -> None:
-    announce(f"saving forward vs forward, batch={batch}, waves={waves}")
+def test_saving_forward_is_bitwise_the_forward(batch: int, waves: str | None) -> None:
+    """waves None: each forward with its default workgroup (12 waves plain, 8 saving); else both
+    forced to that many waves."""
+    announce(f"saving forward vs forward, batch={batch}, waves={waves or 'default'}")
     from fused_hoad import fused_forward_laplacian
 
     p = packed(0)
     x = coordinates(batch, seed=41)
-    with knobs(FUSED_HOAD_FWD_WAVES=waves):
+    with knobs(**({} if waves is None else {"FUSED_HOAD_FWD_WAVES": waves})):
         u, lap = fused_forward_laplacian(x, p, 2)
         su, slap, saved = _saving_forward(x, p)
     torch.cuda.synchronize()
