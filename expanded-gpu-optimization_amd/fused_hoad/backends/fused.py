@@ -50,7 +50,11 @@ _cache: dict[str, object] = {}
 
 
 class FusedForwardLaplacian(torch.autograd.Function):
-    """Fused-kernel forward; fused-kernel (or, by name, recompute) backward."""
+    """Fused-kernel forward; fused-kernel (or, by name, recompute) backward, over a packed
+    parameter buffer (the reference's public Function, same arguments). ``fused_laplacian``
+    runs it for the ``"recompute"`` mode of a model as built; its ``"cuda*"`` and ``"saved"``
+    modes run the C++ Function behind ``_C._model_laplacian``, which gives bitwise the same
+    results."""
 
     @staticmethod
     def forward(ctx, coordinates: Tensor, parameters: Tensor, version: int, backward: str):
