@@ -2574,7 +2574,12 @@ extern "C" int fhoad_forward_laplacian(const float* coordinates, const float* pa
 
 extern "C" size_t fhoad_saved_layers_size(int64_t batch) {
   if (batch <= 0) return 0;
-  return static_cast<size_t>((batch + kTile - 1) / kTile) * kSavedF4PerTile * sizeof(f4);
+  // Unsigned, and saturated: a batch whose buffer would not fit in size_t gets SIZE_MAX, which
+  // no buffer can hold, so the saving forward rejects it.
+  constexpr uint64_t kTileBytes = static_cast<uint64_t>(kSavedF4PerTile) * sizeof(f4);
+  const uint64_t tiles = (static_cast<uint64_t>(batch) + kTile - 1) / kTile;
+  if (tiles > SIZE_MAX / kTileBytes) return SIZE_MAX;
+  return static_cast<size_t>(tiles * kTileBytes);
 }
 
 extern "C" int fhoad_forward_laplacian_saving(const float* coordinates, const float* parameters,

@@ -177,9 +177,13 @@ def test_saved_layers_size() -> None:
     lib = _lib()
     assert lib.fhoad_saved_layers_size(0) == 0
     assert lib.fhoad_saved_layers_size(-5) == 0
-    for batch in (1, 15, 16, 17, 65536, 70001, 1 << 31):
+    for batch in (1, 15, 16, 17, 65536, 70001, 1 << 31, 1 << 40):
         assert lib.fhoad_saved_layers_size(batch) == -(-batch // 16) * 49152, batch
     assert lib.fhoad_saved_layers_size(65536) == 65536 * 3 * 64 * 4 * 4
+    # a buffer size past size_t saturates (no buffer holds it), as does the largest batch
+    size_max = (1 << 64) - 1
+    assert lib.fhoad_saved_layers_size(1 << 62) == size_max
+    assert lib.fhoad_saved_layers_size((1 << 63) - 1) == size_max
 
 
 def test_torch_extension_reports_contract_errors_on_cpu() -> None:
