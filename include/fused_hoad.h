@@ -113,7 +113,8 @@ int fhoad_forward_laplacian_backward_noalloc(const float* coordinates, const flo
 /*
  * Bytes of the saved-layer buffer fhoad_forward_laplacian_saving writes for `batch` points:
  * 49,152 bytes (the three hidden layers' outputs, 4 jet components x 64 neurons each) per
- * 16-point tile, ceil(batch / 16) tiles, i.e. 3 KB per point. 0 for batch <= 0.
+ * 16-point tile, ceil(batch / 16) tiles, i.e. 3 KB per point. 0 for batch <= 0; SIZE_MAX when
+ * the size does not fit in size_t (no buffer can then be large enough).
  */
 size_t fhoad_saved_layers_size(int64_t batch);
 
