@@ -294,11 +294,12 @@ def main() -> None:
         f"saved pair {(pair_ms['saving_forward'] + pair_ms['saved_backward']) * 1e3:.1f} us; bitwise the same results")
 
     # ---- training step (a): the reference's step through the drop-in API ----
-    # fused forward (autograd.Function) + mean((Lap u - f)^2) + fused backward + torch Adam
-    # (/root/reference/benchmarks/benchmark_training.py:41-60). train_step_autograd_ms runs it
-    # on a model flattened once with flatten_poisson_parameters_ (its parameters become views
-    # of the packed buffer, so fused_laplacian packs nothing per step);
-    # train_step_autograd_unflattened_ms on the model as built (a torch.cat pack per step).
+    # fused forward (the C++ autograd Function behind fused_laplacian) + mean((Lap u - f)^2) +
+    # fused backward + torch Adam (/root/reference/benchmarks/benchmark_training.py:41-60).
+    # train_step_autograd_ms runs it on a model flattened once with flatten_poisson_parameters_
+    # (its parameters become views of the packed buffer, so fused_laplacian packs nothing per
+    # step); train_step_autograd_unflattened_ms on the model as built (one pack copy per step,
+    # inside the Function).
     source = manufactured_source(x_train)
 
     def autograd_timing(flatten: bool) -> float:
