@@ -128,7 +128,7 @@ def test_split_forward_is_bitwise_equal_to_the_tiled_kernel(batch: int, scale: f
 @pytest.mark.parametrize(
     "batch,scale,waves",
     [(16401, 1.0, "12"), (65537, 1.0, "12"), (70000, 3.0, "12"), (100000, 1.0, "12"),
-     (262145, 1.0, "12"), (70000, 1.0, "8")],
+     (262145, 1.0, "12"), (70000, 1.0, "8"), (81904, 1.0, "12"), (81904, 3.0, "8")],
 )
 def test_forward_split_rest_is_bitwise_equal_to_whole_tiles(batch: int, scale: float, waves: str) -> None:
     """Past the last whole round (one 16-point tile per SIMD), the tiled kernel runs the
@@ -136,8 +136,9 @@ def test_forward_split_rest_is_bitwise_equal_to_whole_tiles(batch: int, scale: f
     an LDS counter; FUSED_HOAD_FWD_SPLIT_REST=0 runs them as whole tiles. The split tiles run
     the whole tiles' MFMA chains and tanh updates in the same order, so the outputs are bitwise
     equal. 16,401 points leave two split tiles after one round; 70,000 points put two split
-    tiles on some workgroups (two passes through both exchange buffers); scale 3 saturates the
-    tanh; 8-wave workgroups use waves 4-7 as the quad."""
+    tiles on some workgroups (two passes through both exchange buffers); 81,904 points leave
+    1,023 split tiles, four on all but one workgroup (twelve meetings a quad); scale 3
+    saturates the tanh; 8-wave workgroups use waves 4-7 as the quad."""
     announce(f"forward split rest tiles vs whole tiles, batch={batch}, weights x{scale}, waves={waves}")
     p = packed(0) * scale
     x = coordinates(batch, seed=29)

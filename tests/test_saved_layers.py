@@ -34,7 +34,8 @@ def _saving_forward(x, p):
 @pytest.mark.parametrize(
     "batch,waves",
     [(1, None), (17, None), (1000, None), (8192, None), (16401, None), (65536, None),
-     (65537, None), (70000, None), (262145, None), (65536, "12"), (70000, "12"), (70000, "8")],
+     (65537, None), (70000, None), (81904, None), (262145, None), (65536, "12"), (70000, "12"),
+     (70000, "8")],
 )
 def test_saving_forward_is_bitwise_the_forward(batch: int, waves: str | None) -> None:
     """waves None: each forward with its default workgroup (12 waves plain, 8 saving); else both
