@@ -56,7 +56,22 @@ POISSON_PARAMETER_COUNT: int = POISSON_PARAMETER_LAYOUT[-1].end_offset
 
 
 def _linear_layers(model: nn.Module) -> list[nn.Linear]:
-    return [module for module in model.modules() if isinstance(module, nn.Linear)]
+    """The model's ``nn.Linear`` modules in ``model.modules()`` order (pre-order, each module
+    once), walked through ``_modules`` directly: half the host time of ``modules()``, which
+    builds every module's name on the way. The autograd path walks the model every step."""
+    layers: list[nn.Linear] = [model] if isinstance(model, nn.Linear) else []
+    _collect_linear(model, {model}, layers)
+    return layers
+
+
+def _collect_linear(module: nn.Module, seen: set[nn.Module], layers: list[nn.Linear]) -> None:
+    for child in module._modules.values():
+        if child is None or child in seen:
+            continue
+        seen.add(child)
+        if isinstance(child, nn.Linear):
+            layers.append(child)
+        _collect_linear(child, seen, layers)
 
 
 def poisson_parameter_tensors(model: nn.Module) -> list[Tensor]:
@@ -67,15 +82,28 @@ def poisson_parameter_tensors(model: nn.Module) -> list[Tensor]:
         raise ValueError(f"expected {len(POISSON_PARAMETER_LAYOUT)} linear layers")
     tensors: list[Tensor] = []
     for layer, spec in zip(layers, POISSON_PARAMETER_LAYOUT, strict=True):
+        weight, bias = _weight_and_bias(layer)
         expected = (spec.out_features, spec.in_features)
-        if tuple(layer.weight.shape) != expected:
+        if weight.shape != expected:
             raise ValueError(
-                f"{spec.name}.weight must have shape {expected}, got {tuple(layer.weight.shape)}"
+                f"{spec.name}.weight must have shape {expected}, got {tuple(weight.shape)}"
             )
-        if layer.bias is None or tuple(layer.bias.shape) != (spec.out_features,):
+        if bias is None or bias.shape != (spec.out_features,):
             raise ValueError(f"{spec.name}.bias must have shape ({spec.out_features},)")
-        tensors += (layer.weight, layer.bias)
+        tensors += (weight, bias)
     return tensors
+
+
+def _weight_and_bias(layer: nn.Linear) -> tuple[Tensor, Tensor | None]:
+    """``(layer.weight, layer.bias)``, read from the registered parameters when they are there
+    (Module.__getattr__ costs about half a microsecond per read, and the autograd path reads
+    every layer on every step)."""
+    registered = layer._parameters
+    weight = registered.get("weight")
+    if weight is None:
+        weight = layer.weight
+    bias = registered.get("bias") if "bias" in registered else layer.bias
+    return weight, bias
 
 
 def _segments(model: nn.Module) -> list[Tensor]:
@@ -148,10 +176,18 @@ def flattened_poisson_binding(model: nn.Module) -> tuple[Tensor, list[Tensor]] |
     base = flat.data_ptr()
     item = flat.element_size()
     tensors: list[Tensor] = []
-    for layer, spec in zip(_linear_layers(model), POISSON_PARAMETER_LAYOUT, strict=True):
-        weight, bias = layer.weight, layer.bias
+    layers = _linear_layers(model)
+    if len(layers) != len(POISSON_PARAMETER_LAYOUT):
+        return None
+    for layer, spec in zip(layers, POISSON_PARAMETER_LAYOUT):
+        # The registered parameters themselves (what ``layer.weight`` returns, without
+        # Module.__getattr__); a layer that keeps them elsewhere is not a flattened one.
+        weight = layer._parameters.get("weight")
+        bias = layer._parameters.get("bias")
         if (
-            weight.data_ptr() != base + item * spec.weight_offset
+            weight is None
+            or bias is None
+            or weight.data_ptr() != base + item * spec.weight_offset
             or bias.data_ptr() != base + item * spec.bias_offset
         ):
             return None

@@ -88,6 +88,50 @@ def test_pack_round_trip_and_differentiable_pack() -> None:
         pack_poisson_parameters(torch.nn.Sequential(torch.nn.Linear(2, 64)))
 
 
+def test_layer_walk_and_flattened_binding_track_the_model() -> None:
+    """The per-step module walk finds the linear layers in ``model.modules()`` order (nested,
+    shared and ``None`` children included), and the flattened binding holds only while every
+    parameter is a view of the packed buffer at its layout offset."""
+    from torch import nn
+
+    from fused_hoad.parameters import (
+        _linear_layers,
+        flatten_poisson_parameters_,
+        flattened_poisson_binding,
+        poisson_parameter_tensors,
+    )
+
+    shared = nn.Linear(3, 3)
+    nested = nn.Sequential(
+        nn.Linear(2, 2),
+        nn.Sequential(shared, nn.Tanh(), nn.Sequential(nn.Linear(4, 4))),
+        shared,
+        nn.ModuleList([nn.Linear(5, 5), shared]),
+    )
+    nested.add_module("empty", None)
+    for module in (nested, nn.Linear(2, 2), nn.Tanh(), build_mlp(DEFAULT_POISSON_MLP)):
+        assert _linear_layers(module) == [m for m in module.modules() if isinstance(m, nn.Linear)]
+
+    torch.manual_seed(0)
+    model = build_mlp(DEFAULT_POISSON_MLP)
+    assert flattened_poisson_binding(model) is None
+    flat = flatten_poisson_parameters_(model)
+    binding = flattened_poisson_binding(model)
+    assert binding is not None and binding[0] is flat
+    assert all(a is b for a, b in zip(binding[1], model.parameters(), strict=True))
+    assert all(a is b for a, b in zip(poisson_parameter_tensors(model), model.parameters(), strict=True))
+    with torch.no_grad():
+        model[4].bias.data = model[4].bias.detach().clone()  # no longer a view of the buffer
+    assert flattened_poisson_binding(model) is None
+    flatten_poisson_parameters_(model)
+    assert flattened_poisson_binding(model) is not None
+    model[4] = nn.Linear(64, 64)  # a replaced layer is not in the buffer
+    assert flattened_poisson_binding(model) is None
+    model[4] = nn.Linear(64, 63)
+    with pytest.raises(ValueError, match=r"layer2.weight must have shape \(64, 64\), got \(63, 64\)"):
+        poisson_parameter_tensors(model)
+
+
 def test_registry_and_unknown_backend() -> None:
     assert REFERENCE_BACKEND in BACKENDS
     assert set(TRAINABLE_BACKENDS) <= set(BACKENDS)
