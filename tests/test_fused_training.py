@@ -193,6 +193,62 @@ def test_public_python_function_equals_fused_laplacian(mode: str) -> None:
         assert torch.equal(a, b), index
 
 
+@pytest.mark.parametrize("flatten", [False, True])
+@pytest.mark.parametrize("mode", ["cuda", "saved"])
+def test_retained_graph_and_two_calls_accumulate(mode: str, flatten: bool) -> None:
+    """The C++ autograd Function's saved state and gradient views under accumulation:
+    * backward twice through one graph (retain_graph=True) gives each gradient twice its
+      single-backward value, bitwise (g + g = 2 g in float32);
+    * one loss over two calls on the same model (two Function nodes, each handing the
+      parameters views of its own packed gradient) gives the sum of the two calls' gradients,
+      taken separately, bitwise (one float32 addition per entry, which commutes)."""
+    announce(f"retain_graph twice and two calls in one loss, backward={mode}, flattened={flatten}")
+    from fused_hoad import manufactured_source
+    from fused_hoad.backends.fused import fused_laplacian
+    from fused_hoad.parameters import flatten_poisson_parameters_
+
+    xa, xb = coordinates(1500, seed=35), coordinates(2600, seed=36)
+    fa, fb = manufactured_source(xa), manufactured_source(xb)
+
+    def model():
+        m = _model(9)
+        if flatten:
+            flatten_poisson_parameters_(m)
+        return m
+
+    def loss(m, x, f):
+        u, lap = fused_laplacian(m, x, backward=mode)
+        return (lap - f).pow(2).mean() + 0.1 * u.pow(2).mean()
+
+    def grads(m, *extra):
+        return [p.grad.clone() for p in m.parameters()] + [t.grad.clone() for t in extra]
+
+    once = model()
+    xg = xa.clone().requires_grad_(True)
+    loss(once, xg, fa).backward()
+    single = grads(once, xg)
+    twice = model()
+    xg2 = xa.clone().requires_grad_(True)
+    value = loss(twice, xg2, fa)
+    value.backward(retain_graph=True)
+    value.backward()
+    doubled = grads(twice, xg2)
+
+    separate = []
+    for x, f in ((xa, fa), (xb, fb)):
+        m = model()
+        loss(m, x, f).backward()
+        separate.append(grads(m))
+    both = model()
+    (loss(both, xa, fa) + loss(both, xb, fb)).backward()
+    summed = grads(both)
+    torch.cuda.synchronize()
+    for index, (a, b) in enumerate(zip(doubled, single, strict=True)):
+        assert torch.equal(a, 2 * b), f"retain_graph: gradient {index}"
+    for index, (a, b, c) in enumerate(zip(summed, *separate, strict=True)):
+        assert torch.equal(a, b + c), f"two calls: gradient {index}"
+
+
 def test_fused_trains_like_forward_laplacian() -> None:
     announce("50 Adam steps, fused vs forward_laplacian, batch=2048")
     from fused_hoad import forward_laplacian, get_backend
