@@ -131,6 +131,23 @@ def test_layer_walk_and_flattened_binding_track_the_model() -> None:
     with pytest.raises(ValueError, match=r"layer2.weight must have shape \(64, 64\), got \(63, 64\)"):
         poisson_parameter_tensors(model)
 
+    # A parametrized weight is not a registered parameter: it is read through the module (its
+    # computed value), and gradients reach the parametrization's original.
+    from torch.nn.utils import parametrize
+
+    class Doubled(nn.Module):
+        def forward(self, weight):
+            return 2 * weight
+
+    torch.manual_seed(0)
+    model = build_mlp(DEFAULT_POISSON_MLP)
+    before = model[2].weight.detach().clone()
+    parametrize.register_parametrization(model[2], "weight", Doubled())
+    assert torch.equal(poisson_parameter_tensors(model)[2], 2 * before)
+    pack_poisson_parameters(model, differentiable=True).sum().backward()
+    original = model[2].parametrizations.weight.original
+    assert torch.equal(original.grad, torch.full_like(original, 2.0))
+
 
 def test_registry_and_unknown_backend() -> None:
     assert REFERENCE_BACKEND in BACKENDS
