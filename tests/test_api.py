@@ -149,6 +149,20 @@ def test_layer_walk_and_flattened_binding_track_the_model() -> None:
     assert torch.equal(original.grad, torch.full_like(original, 2.0))
 
 
+def test_bench_runs_on_one_gpu_only() -> None:
+    """bench.py --gpus N with N > 1 exits (status 2) with a message, before touching a GPU."""
+    import subprocess
+    import sys
+
+    result = subprocess.run(
+        [sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+        capture_output=True, text=True, timeout=300, cwd=ROOT,
+    )
+    assert result.returncode == 2
+    assert "one GPU only" in result.stdout + result.stderr
+    assert not result.stdout.strip()  # no JSON line
+
+
 def test_registry_and_unknown_backend() -> None:
     assert REFERENCE_BACKEND in BACKENDS
     assert set(TRAINABLE_BACKENDS) <= set(BACKENDS)
