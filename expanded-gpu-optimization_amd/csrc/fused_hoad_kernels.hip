@@ -91,30 +91,18 @@ constexpr int kSmallFloats = kSmallBout + 4;
 __device__ __forceinline__ int lane_rows(int m, int g) { return kWRow * m + 4 * g; }
 __device__ __forceinline__ int lane_cols(int m, int g) { return 272 * g + m; }
 
-// The backward's dW staging planes hold [neuron row R][tile point p] at pitch 80, with the
-// point index XOR-ed with 24 in rows whose bit 2 is set:
-//   (R, p) at 80 R + (p ^ (24 ((R >> 2) & 1))).
-// They are written 4 bytes per lane (lane (m, g): rows 4 g + r of a 16-row block, point m of
-// a 16-point block) and read 16 bytes per lane (row m, points 4 g .. 4 g + 3 of a block).
-// Measured on gfx950 with probe kernels that issue exactly these two patterns
-// (SQ_LDS_BANK_CONFLICT): at pitch 68 without the XOR, as the weight planes are, every 16-byte
-// read costs 4 conflict cycles and the writes none; with this layout neither conflicts. (At
-// pitch 72 with the 16-point blocks swapped on row bit 3 both patterns conflicted.)
-constexpr int kSRow = 80;
-constexpr int kSPlane = 64 * kSRow;
-// Write base of lane (m, g) in wave w: row 4 g (+ 16 mb + r, immediates), point 16 w + m.
-// (4 g + r) >> 2 = g, so the XOR is a lane constant.
-__device__ __forceinline__ int stage_lane_cols(int m, int g, int w) {
-  return 4 * kSRow * g + ((16 * w + m) ^ (24 * (g & 1)));
-}
-// Read base of lane (m, g) for point block ns of row 16 b + m: with t = (m >> 2) & 1 the
-// points 16 ns + 4 g .. + 3 sit at 16 (ns ^ t) + 4 (g ^ 2 t), so even blocks are 16 t floats
-// further and odd blocks 16 t floats nearer than 16 ns. `odd` selects the base for odd ns; ns
-// itself stays an immediate.
-__device__ __forceinline__ int stage_lane_rows(int m, int g, bool odd) {
-  const int t = (m >> 2) & 1;
-  return kSRow * m + 4 * (g ^ (2 * t)) + (odd ? -16 * t : 16 * t);
-}
+// The backward's dW staging buffer: six planes of [neuron row R][tile point p] in the weight
+// planes' layout, (R, p) at 68 R + p. Planes 0..2 hold zbar of the three "early" jet
+// components (early_component(e) in plane e), planes 3..5 h_prev of the same components; the
+// "late" component (J1) goes into planes 0 and 3 once the products of plane pair (0, 3) are done.
+// They are written 4 bytes per lane (lane (m, g) of wave w: rows 4 g + r of a 16-row block, point
+// 16 w + m; base lane_cols(m, g) + 16 w, conflict-free) and read 16 bytes per lane (row m,
+// points 4 g .. 4 g + 3 of a 16-point block; base lane_rows(m, g); 4 bank-conflict cycles per
+// read on gfx950, which overlap the MFMAs that consume them). Six planes at pitch 68 (104 KB)
+// fit beside the 52 KB of weight planes; at the conflict-free pitch 80 only four would.
+constexpr int kStagePlanes = 6;
+__device__ __forceinline__ constexpr int early_component(int e) { return e == 0 ? 0 : e == 1 ? 3 : 1; }
+constexpr int kLateComponent = 2;
 
 __device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -948,9 +936,10 @@ forward_split_kernel(const float* __restrict__ coordinates, const float* __restr
 //      tanh-jet adjoint from h in registers (tanh_jet_adjoint_h, no tanh re-evaluated),
 //      dW += zbar h_prev^T, hbar = W^T zbar one input block at a time (registers), and
 //      finally layer 0 in closed form;
-//   3. dW contracts over the points of all 4 waves: zbar and h_prev are staged in LDS (two
-//      components at a time) and wave w owns output rows 16 w .. 16 w + 15 of every dW; the
-//      hidden bias gradients fall out of the same LDS reads. W0, b0 and w_out gradients are
+//   3. dW contracts over the points of all 4 waves: zbar and h_prev are staged in LDS (three
+//      jet components written behind the MFMAs of the phase before, the fourth behind the first
+//      components' dW MFMAs; see staged_dw) and wave w owns output rows 16 w .. 16 w + 15 of
+//      every dW; the hidden bias gradients fall out of the same LDS reads. W0, b0 and w_out gradients are
 //      summed over each wave's points in registers (row_reduce_scatter16) and over the 4 waves once
 //      per slot.
 // Weight gradients accumulate in registers across the tiles of a "slot": slot s takes the
@@ -966,57 +955,83 @@ static_assert(kMaxSlots % kReduceGroups == 0, "reduction tree must tile the slot
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
-// Stage two jet components of this wave's zbar and h_prev into the dW staging buffer: planes
-// of [neuron][tile point] (kSRow layout), so this lane's value of neuron 16 mb + 4 g + r at
-// point 16 w + m lands at stage_lane + 16 kSRow mb + kSRow r (stage_lane_cols holds the swap).
-// zbar components go to planes 0, 1 and h_prev components to planes 2, 3.
-__device__ __forceinline__ void stage_write(float* stage_lane, int mb, int r, float z_a,
-                                            float z_b, float h_a, float h_b) {
-  float* p = stage_lane + 16 * kSRow * mb + kSRow * r;
-  p[0] = z_a;
-  p[kSPlane] = z_b;
-  p[2 * kSPlane] = h_a;
-  p[3 * kSPlane] = h_b;
+// Staging bases of one lane, formed where each phase starts (from opaque copies of the lane
+// offsets, see backward_kernel): writes of zbar (planes 0..2) and h_prev (planes 3..5) at rows
+// 4 g + r of a block and point 16 w + m; reads of the A operand (this wave's rows 16 w + m, zbar
+// planes) and of the B operands (rows 16 n + m, h_prev planes) at points 4 g .. 4 g + 3 of a
+// 16-point block. Every other offset is an instruction immediate (planes 0..2 from a base stay
+// within a DS offset's 64 KB reach, hence the second base for planes 3..5).
+struct StageBases {
+  float* wz;
+  float* wh;
+  const float* ra;
+  const float* rb;
+};
+
+// Staging write i (0..23) of block mb: the three early components of zbar (x, planes 0..2) and
+// of h_prev (y, planes 3..5), alternating, for this lane's rows 16 mb + 4 g + r.
+__device__ __forceinline__ void stage_early_write(const StageBases& sb, int mb, const f4 (&x)[4],
+                                                  const f4 (&y)[4], int i) {
+  const int e = i >> 3, r = (i >> 1) & 3;
+  float* base = (i & 1) ? sb.wh : sb.wz;
+  base[e * kPlane + kWRow * (16 * mb + r)] = (i & 1) ? y[early_component(e)][r] : x[early_component(e)][r];
 }
 
-// dW[16 w + ., 16 nb + .] += sum over (2 staged components, 64 points) of zbar h_prev^T.
-// Lane (m, g) reads zbar[16 w + m][p] and h_prev[16 nb + m][p] for p = 16 s + 4 g + k,
-// k = 0..3, as 16-byte reads (rows_even / rows_odd: stage_lane_rows for even / odd s), so the
-// MFMA contracts over points; every lane supplies the same points at each step. Returns the
-// sum of this lane's plane-0 zbar reads (the bias gradient partial when plane 0 holds zbar_v).
-__device__ __forceinline__ float dw_product(const float* rows_even, const float* rows_odd, int w,
-                                            f4 (&dw)[4]) {
+// Staging write i (0..31) of the late component: zbar (xl[mb], plane 0) and h_prev (yl[mb],
+// plane 3), alternating, rows 16 mb + 4 g + r.
+__device__ __forceinline__ void stage_late_write(const StageBases& sb, const f4 (&xl)[4],
+                                                 const f4 (&yl)[4], int i) {
+  const int mb = i >> 3, r = (i >> 1) & 3;
+  float* base = (i & 1) ? sb.wh : sb.wz;
+  base[kWRow * (16 * mb + r)] = (i & 1) ? yl[mb][r] : xl[mb][r];
+}
+
+// dW[16 w + ., 16 n + .] += sum over the 64 tile points of zbar_c h_prev_c^T for the components
+// staged in plane pairs (kFirst + i, kFirst + 3 + i), i < kN. Step s of a component reads the A
+// operand zbar[16 w + m][p] and the B operands h_prev[16 n + m][p] for p = 16 s + 4 g + k,
+// k = 0..3 (16-byte reads, one step ahead), and its 16 MFMAs contract over those points; every
+// lane supplies the same points at each step. emit(step, k) issues staging writes after the
+// MFMAs of point k: they follow the next step's reads, so waiting for those reads never waits for
+// them, and they drain behind the MFMAs. With kBias, returns the sum of this lane's reads of the
+// first component (the hidden bias gradient's partial for row 16 w + m when it is zbar_v).
+template <int kFirst, int kN, bool kBias, typename Emit>
+__device__ __forceinline__ float dw_pass(const StageBases& sb, f4 (&dw)[4], Emit emit) {
   float bias = 0.0f;
-  // Steps (cc, s) in order; each step's five 16-byte operands are read one step ahead.
   f4 na, nb[4];
-  na = lds4(rows_even + 16 * kSRow * w);
+  auto read = [&](int step, f4& a, f4 (&b)[4]) {
+    const int plane = kFirst + (step >> 2), s = step & 3;
+    a = lds4(sb.ra + plane * kPlane + 16 * s);
 #pragma unroll
-  for (int b = 0; b < 4; ++b) nb[b] = lds4(rows_even + 2 * kSPlane + 16 * kSRow * b);
+    for (int n = 0; n < 4; ++n) b[n] = lds4(sb.rb + plane * kPlane + 16 * kWRow * n + 16 * s);
+  };
+  read(0, na, nb);
 #pragma unroll
-  for (int step = 0; step < 8; ++step) {
-    const int cc = step >> 2;
+  for (int step = 0; step < 4 * kN; ++step) {
     const f4 a = na;
     f4 b[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) b[k] = nb[k];
-    if (step < 7) {
-      const int ncc = (step + 1) >> 2, ns = (step + 1) & 3;
-      const float* rows = (ns & 1) ? rows_odd : rows_even;
-      na = lds4(rows + ncc * kSPlane + 16 * kSRow * w + 16 * ns);
+    for (int n = 0; n < 4; ++n) b[n] = nb[n];
+    if (kBias && step < 4) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) nb[k] = lds4(rows + (2 + ncc) * kSPlane + 16 * kSRow * k + 16 * ns);
+      for (int k = 0; k < 4; ++k) bias += a[k];
     }
+    if (step + 1 < 4 * kN) read(step + 1, na, nb);
     lds_mfma_fence();
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      if (cc == 0) bias += a[k];
 #pragma unroll
       for (int n = 0; n < 4; ++n) dw[n] = mfma(a[k], b[n][k], dw[n]);
+      if (emit(step, k)) __builtin_amdgcn_sched_barrier(0);
     }
     lds_mfma_fence();
   }
   return bias;
 }
+
+// emit() that issues nothing.
+struct NoEmit {
+  __device__ __forceinline__ bool operator()(int, int) const { return false; }
+};
 
 // Per-neuron sums over a wave's 16 points without LDS: lane (m, g) holds x for neuron
 // 16 mb + 4 g + r at point m, so summing value k = 4 mb + r over the 16 lanes of row g gives
@@ -1025,44 +1040,25 @@ __device__ __forceinline__ float dw_product(const float* rows_even, const float*
 // own the 64 neurons once each.
 __device__ __forceinline__ int owned_neuron(int m, int g) { return 16 * (m >> 2) + 4 * g + (m & 3); }
 
-// dW1 += zbar1 h0^T over the workgroup tile, in two passes of two jet components: (v, L) first,
-// then (J0, J1). h0 is layer 0's output, rebuilt from its closed form
-// z' = (c (W0 x + b0), 2 W0[:,0], 2 W0[:,1], 0); its (v', s') are returned in (pv, ps) for
-// layer 0's own adjoint. Adds the bias gradient sum_p zbar_v' = sum_p zbar_v / c to g_bias.
-__device__ __forceinline__ void stage_and_dw_layer0(const f4 (&zbar)[4][4], f4 (&dw)[4],
-                                                    float& g_bias, float* stage_lane,
-                                                    const float* rows_even, const float* rows_odd,
-                                                    const float* s_small,
-                                                    int w, int g, float x0, float x1,
-                                                    f4 (&pv)[4], f4 (&ps)[4]) {
-  __syncthreads();  // previous readers of the staging buffer are done
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const Layer0Weights w0 = layer0_weights(s_small, mb, g);
-    f4 zv;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) zv[r] = layer0_zv(w0, r, x0, x1);
-    tanh_scaled4(zv, pv[mb], ps[mb]);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float v = pv[mb][r];
-      stage_write(stage_lane, mb, r, zbar[mb][0][r], zbar[mb][3][r], v, ps[mb][r] * (v * w0.q[r]));
-    }
-  }
-  __syncthreads();
-  g_bias += sum_lane_groups(dw_product(rows_even, rows_odd, w, dw));
-  __syncthreads();
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const Layer0Weights w0 = layer0_weights(s_small, mb, g);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      stage_write(stage_lane, mb, r, zbar[mb][1][r], zbar[mb][2][r], ps[mb][r] * w0.wx[r],
-                  ps[mb][r] * w0.wy[r]);
-    }
-  }
-  __syncthreads();
-  dw_product(rows_even, rows_odd, w, dw);
+// dW += zbar h_prev^T over the workgroup tile from the staged planes, once the early components
+// of zbar and h_prev are written (planes 0..2, 3..5) and the late ones are in registers (xl: zbar,
+// yl: h_prev, per block):
+//   barrier; component e = 0 (zbar_v: the bias sum); barrier (every wave is done with planes 0
+//   and 3); components e = 1, 2, with the late component's writes into planes 0 and 3 between
+//   their MFMAs; barrier; the late component.
+// Adds sum_p zbar_v' of row 16 w + m (all lane groups) to g_bias. The products accumulate in the
+// component order v, L, J0, J1 and point order of each, as two passes of (v, L), (J0, J1) did.
+__device__ __forceinline__ void staged_dw(const StageBases& sb, const f4 (&xl)[4], const f4 (&yl)[4],
+                                          f4 (&dw)[4], float& g_bias) {
+  __syncthreads();  // the early components are written
+  g_bias += sum_lane_groups(dw_pass<0, 1, true>(sb, dw, NoEmit{}));
+  __syncthreads();  // every wave is done with planes 0 and 3
+  dw_pass<1, 2, false>(sb, dw, [&](int step, int k) {
+    stage_late_write(sb, xl, yl, 4 * step + k);
+    return true;
+  });
+  __syncthreads();  // the late component is written
+  dw_pass<0, 1, false>(sb, dw, NoEmit{});
 }
 
 // ---- the interior tiles of backward_kernel: the walk back from each layer's tanh-jet output ----
@@ -1121,9 +1117,12 @@ __device__ __forceinline__ void tanh_jet_adjoint_h_seed(float v, float hj0, floa
 // hidden_product_native); a block's tanh jet (VALU) and the next block's 64 MFMAs are independent,
 // so either can fill the other's latencies. The next block's four A operands (16-byte LDS
 // reads) are issued before this block's MFMAs, so no block waits for LDS. w_rows is this
-// lane's row base (68 m + 4 g).
+// lane's row base (68 m + 4 g). emit(mb, k) may issue LDS writes after k-step k (0..15) of
+// block mb's MFMAs (returning whether it did), behind the next block's reads.
+template <typename Emit = NoEmit>
 __device__ __forceinline__ void forward_layer(const float* s_small, const float* w_rows, int layer,
-                                              int g, const f4 (&hin)[4][4], f4 (&hout)[4][4]) {
+                                              int g, const f4 (&hin)[4][4], f4 (&hout)[4][4],
+                                              Emit emit = Emit{}) {
   f4 bias[4];
   load_bias(s_small, layer, g, bias);
   const float* w = w_rows + layer * kPlane;
@@ -1150,6 +1149,7 @@ __device__ __forceinline__ void forward_layer(const float* s_small, const float*
           const f4 cin = (ob | j) ? z[c] : (c == 0 ? bias[mb] : zero4());
           z[c] = mfma(a[ob][j], hin[ob][c][j], cin);
         }
+        if (emit(mb, 4 * ob + j)) __builtin_amdgcn_sched_barrier(0);
       }
     }
     lds_mfma_fence();  // the next block's reads stay ahead of this block's MFMAs
@@ -1182,9 +1182,13 @@ __device__ __forceinline__ void transposed_block(const float (&a)[16], const f4 
 // The adjoint through one hidden layer's weights and the tanh jet below it, one input block at
 // a time: hbar = W^T zbar for block ib, then the tanh-jet adjoint of that block of the layer
 // below, from its output hp, which replaces hp[ib] by the layer below's zbar. Only one block of
-// hbar is live at a time.
+// hbar is live at a time. after(ib) runs once block ib's adjoint is done (VALU work of the caller
+// for that block); emit(ib, step) may issue LDS writes of block ib after k-step `step` of block
+// ib + 1's MFMAs (returning whether it did), behind block ib + 2's operand reads, and block 3's
+// writes follow its adjoint.
+template <typename After, typename Emit>
 __device__ __forceinline__ void adjoint_through(const float* w, const f4 (&zb)[4][4],
-                                                f4 (&hp)[4][4]) {
+                                                f4 (&hp)[4][4], After after, Emit emit) {
   float next[16];
   transposed_operands(w, 0, next);
 #pragma unroll
@@ -1195,7 +1199,14 @@ __device__ __forceinline__ void adjoint_through(const float* w, const f4 (&zb)[4
     if (ib < 3) transposed_operands(w, ib + 1, next);
     lds_mfma_fence();
     f4 hb[4];
-    transposed_block(a, zb, hb);
+#pragma unroll
+    for (int step = 0; step < 16; ++step) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        hb[c] = mfma(a[step], zb[step >> 2][c][step & 3], step ? hb[c] : zero4());
+      }
+      if (ib > 0 && emit(ib - 1, step)) __builtin_amdgcn_sched_barrier(0);
+    }
     lds_mfma_fence();
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -1206,36 +1217,20 @@ __device__ __forceinline__ void adjoint_through(const float* w, const f4 (&zb)[4
       hp[ib][2][r] = bj1;
       hp[ib][3][r] = bl;
     }
+    after(ib);
   }
+#pragma unroll
+  for (int step = 0; step < 16; ++step) emit(3, step);
 }
 
-// dW += zbar h_prev^T over the workgroup tile (stage_and_dw with h_prev given, not rebuilt):
-// two passes of two jet components, (v, L) then (J0, J1). Adds the bias gradient sum
-// sum_p zbar_v' to g_bias.
-__device__ __forceinline__ void stage_and_dw_h(const f4 (&zbar)[4][4], const f4 (&hp)[4][4],
-                                               f4 (&dw)[4], float& g_bias, float* stage_lane,
-                                               const float* rows_even, const float* rows_odd,
-                                               int w) {
-  __syncthreads();  // previous readers of the staging buffer are done
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      stage_write(stage_lane, mb, r, zbar[mb][0][r], zbar[mb][3][r], hp[mb][0][r], hp[mb][3][r]);
-    }
-  }
-  __syncthreads();
-  g_bias += sum_lane_groups(dw_product(rows_even, rows_odd, w, dw));
-  __syncthreads();
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      stage_write(stage_lane, mb, r, zbar[mb][1][r], zbar[mb][2][r], hp[mb][1][r], hp[mb][2][r]);
-    }
-  }
-  __syncthreads();
-  dw_product(rows_even, rows_odd, w, dw);
+// Staging writes of a block's early components spread over the 16 k-steps of a block of MFMAs:
+// writes 2 step and 2 step + 1 of stage_early_write after k-step `step` < 12.
+__device__ __forceinline__ bool emit_early_pair(const StageBases& sb, int mb, const f4 (&x)[4],
+                                                const f4 (&y)[4], int step) {
+  if (step >= 12) return false;
+  stage_early_write(sb, mb, x, y, 2 * step);
+  stage_early_write(sb, mb, x, y, 2 * step + 1);
+  return true;
 }
 
 // Seed of the fused Poisson training step (kLoss). The loss is the PINN loss
@@ -1266,7 +1261,7 @@ static_assert(kLossColumn + 1 < kRowStride, "the loss columns must fit in a part
 // Per-slot gradient sums of one wave (see backward_kernel).
 struct WaveSums {
   f4 dw[3][4];         // hidden dW, rows 16 w + ., in MFMA accumulator layout
-  float bh[3];         // hidden bias sums of c^-1 zbar_v (this lane's neuron, see dw_product)
+  float bh[3];         // hidden bias sums of c^-1 zbar_v (row 16 w + m, see dw_pass)
   float w0x, w0y, b0;  // layer-0 sums, lane = owned neuron
   float wout, bout;    // output-layer sums
   float loss, bloss;   // kLoss: sums of r^2 and u_b^2
@@ -1292,7 +1287,7 @@ constexpr int kBndPitch = 20;                                   // transposed ro
 constexpr int kBndExchange = 0;                                 // [2][4 waves][64 lanes] f4
 constexpr int kBndH = kBndExchange + 2 * kBwdWaves * kWave * 4;  // [3 layers][64 rows][pitch]
 constexpr int kBndZ = kBndH + 3 * kHidden * kBndPitch;          // [2][4 waves][16 rows][pitch]
-static_assert(kBndZ + 2 * kBwdWaves * 16 * kBndPitch <= 4 * kSPlane,
+static_assert(kBndZ + 2 * kBwdWaves * 16 * kBndPitch <= kStagePlanes * kPlane,
               "the boundary tile's scratch must fit the dW staging buffer");
 
 // Store this lane's 4 rows row0 + 4 g + r (value at point m) into a transposed buffer.
@@ -1522,7 +1517,7 @@ constexpr int kSplitScratchFloats = 3 * kTPlane + 2 * kSplitWaves * 4 * kWave * 
                                     kSplitWaves * kTWave + kSplitWaves * 2 * kTile;
 
 // Per-lane point sums of split_tile: bias sums go to the caller's array (row 16 w + m, as in
-// dw_product); these are of row 16 w + 4 g + (m & 3) (w0x, w0y, b0, wout), or the same in every
+// dw_pass); these are of row 16 w + 4 g + (m & 3) (w0x, w0y, b0, wout), or the same in every
 // lane of a wave (bout, loss, bloss).
 struct SplitSums {
   float w0x, w0y, b0, wout, bout, loss, bloss;
@@ -1751,8 +1746,9 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
                 int64_t batch, int64_t whole, int64_t tiles, int slots, LossSeed seed,
                 const f4* __restrict__ saved, int64_t saved_tiles) {
   static_assert(!(kLoss && kSaved), "the fused step computes its forward once; nothing to read");
-  constexpr int kStageFloats =
-      kRest && kSplitScratchFloats > 4 * kSPlane ? kSplitScratchFloats : 4 * kSPlane;
+  constexpr int kStageFloats = kRest && kSplitScratchFloats > kStagePlanes * kPlane
+                                   ? kSplitScratchFloats
+                                   : kStagePlanes * kPlane;
   __shared__ __attribute__((aligned(16))) float s_w[3 * kPlane];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ __attribute__((aligned(16))) float s_stage[kStageFloats];
@@ -1778,9 +1774,13 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   // span more than the 64 KB reach of a DS offset, and hoisted bases would be spilled.
   const int rows_off = lane_rows(m, g);
   const int cols_off = lane_cols(m, g);
-  const int stage_lane_off = stage_lane_cols(m, g, w);
-  const int stage_even_off = stage_lane_rows(m, g, false);
-  const int stage_odd_off = stage_lane_rows(m, g, true);
+  const int stage_write_off = cols_off + 16 * w;    // staging writes: point 16 w + m
+  const int stage_a_off = rows_off + 16 * kWRow * w;  // A operand reads: this wave's rows
+  auto stage_bases = [&]() {
+    const int wo = opaque(stage_write_off), ao = opaque(stage_a_off), ro = opaque(rows_off);
+    return StageBases{s_stage + wo, s_stage + 3 * kPlane + wo, s_stage + ao,
+                      s_stage + 3 * kPlane + ro};
+  };
 
   for (int slot = blockIdx.x; slot < slots; slot += gridDim.x) {
     WaveSums acc;
@@ -1838,6 +1838,8 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       const float f = kLoss ? in.a : 0.f;
 
       // ---- 1. forward recompute (kSaved: read ahead, above and in the walk back) ----
+      // h2 is dW3's h_prev: its early components go to the staging planes between hidden layer
+      // 3's MFMAs, once every wave is done with the previous tile's planes.
       if constexpr (!kSaved) {
         {
           f4 h0[4][4];
@@ -1845,7 +1847,23 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
           forward_layer(s_small, s_w + opaque(rows_off), 0, g, h0, h1);
         }
         forward_layer(s_small, s_w + opaque(rows_off), 1, g, h1, h2);
-        forward_layer(s_small, s_w + opaque(rows_off), 2, g, h2, h3);
+      }
+      __syncthreads();  // the previous tile's readers of the staging planes are done
+      const StageBases sb3 = stage_bases();
+      auto stage_h2 = [&](int mb, int step) {
+        if (step >= 12) return false;
+        const int e = step >> 2, r = step & 3;
+        sb3.wh[e * kPlane + kWRow * (16 * mb + r)] = h2[mb][early_component(e)][r];
+        return true;
+      };
+      if constexpr (!kSaved) {
+        forward_layer(s_small, s_w + opaque(rows_off), 2, g, h2, h3, stage_h2);
+      } else {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+          for (int step = 0; step < 12; ++step) stage_h2(mb, step);
+        }
       }
 
       if (kLoss) {
@@ -1889,33 +1907,70 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
             h3[mb][2][r] = bj1;
             h3[mb][3][r] = bl;
           }
+#pragma unroll
+          for (int i = 0; i < 12; ++i) {  // zbar3's early components of this block
+            sb3.wz[(i >> 2) * kPlane + kWRow * (16 * mb + (i & 3))] = h3[mb][early_component(i >> 2)][i & 3];
+          }
         }
         acc.wout += row_reduce_scatter16(wout_terms, m_pick);
         if (!kLoss) acc.bout += sum_row16(gu);
       }
 
       // ---- 3. hidden layer 3: dW3 from (zbar3, h2), then W3^T zbar3 into layer 2's adjoint ----
-      stage_and_dw_h(h3, h2, acc.dw[2], acc.bh[2], s_stage + opaque(stage_lane_off),
-                     s_stage + opaque(stage_even_off), s_stage + opaque(stage_odd_off), w);
-      adjoint_through(s_w + opaque(cols_off) + 2 * kPlane, h3, h2);
+      // The adjoint's blocks of zbar2 and h1 (dW2's operands) are staged behind the MFMAs of the
+      // next block.
+      staged_dw(sb3, {h3[0][kLateComponent], h3[1][kLateComponent], h3[2][kLateComponent], h3[3][kLateComponent]},
+                {h2[0][kLateComponent], h2[1][kLateComponent], h2[2][kLateComponent], h2[3][kLateComponent]},
+                acc.dw[2], acc.bh[2]);
+      __syncthreads();  // every wave is done with the staged planes
+      {
+        const StageBases sb = stage_bases();
+        adjoint_through(s_w + opaque(cols_off) + 2 * kPlane, h3, h2, [](int) {},
+                        [&](int ib, int step) { return emit_early_pair(sb, ib, h2[ib], h1[ib], step); });
+      }
       if constexpr (kSaved) {
         if (has_next) load_saved_layer(saved, next_saved_tile, saved_tiles, 2, lane, h3);
       }
 
       // ---- 4. hidden layer 2: dW2 from (zbar2, h1), then W2^T zbar2 into layer 1's adjoint ----
-      stage_and_dw_h(h2, h1, acc.dw[1], acc.bh[1], s_stage + opaque(stage_lane_off),
-                     s_stage + opaque(stage_even_off), s_stage + opaque(stage_odd_off), w);
-      deliver(next);  // the next tile's inputs, before this tile's stores
-      adjoint_through(s_w + opaque(cols_off) + kPlane, h2, h1);
+      // Layer 0's output h0 (dW1's h_prev) is rebuilt block by block from its closed form
+      // z' = (c (W0 x + b0), 2 W0[:,0], 2 W0[:,1], 0), keeping its (v', s') for layer 0's own
+      // adjoint; the blocks of zbar1 and h0 are staged behind the next block's MFMAs.
+      f4 v0[4], s0[4], h0[4][4];
+      {
+        const StageBases sb = stage_bases();
+        staged_dw(sb, {h2[0][kLateComponent], h2[1][kLateComponent], h2[2][kLateComponent], h2[3][kLateComponent]},
+                  {h1[0][kLateComponent], h1[1][kLateComponent], h1[2][kLateComponent], h1[3][kLateComponent]},
+                  acc.dw[1], acc.bh[1]);
+        deliver(next);  // the next tile's inputs, before this tile's stores
+        __syncthreads();  // every wave is done with the staged planes
+        adjoint_through(
+            s_w + opaque(cols_off) + kPlane, h2, h1,
+            [&](int ib) {
+              const Layer0Weights w0 = layer0_weights(s_small, ib, g);
+              f4 zv;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) zv[r] = layer0_zv(w0, r, x0, x1);
+              tanh_scaled4(zv, v0[ib], s0[ib]);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                h0[ib][0][r] = v0[ib][r];
+                h0[ib][1][r] = s0[ib][r] * w0.wx[r];
+                h0[ib][2][r] = s0[ib][r] * w0.wy[r];
+                h0[ib][3][r] = s0[ib][r] * (v0[ib][r] * w0.q[r]);
+              }
+            },
+            [&](int ib, int step) { return emit_early_pair(sb, ib, h1[ib], h0[ib], step); });
+      }
       if constexpr (kSaved) {
         if (has_next) load_saved_layer(saved, next_saved_tile, saved_tiles, 1, lane, h2);
       }
 
-      // ---- 5. hidden layer 1: dW1 from (zbar1, h0), h0 rebuilt with its (v', s') ----
-      f4 v0[4], s0[4];
-      stage_and_dw_layer0(h1, acc.dw[0], acc.bh[0], s_stage + opaque(stage_lane_off),
-                          s_stage + opaque(stage_even_off), s_stage + opaque(stage_odd_off),
-                          s_small, w, g, x0, x1, v0, s0);
+      // ---- 5. hidden layer 1: dW1 from (zbar1, h0) ----
+      staged_dw(stage_bases(),
+                {h1[0][kLateComponent], h1[1][kLateComponent], h1[2][kLateComponent], h1[3][kLateComponent]},
+                {h0[0][kLateComponent], h0[1][kLateComponent], h0[2][kLateComponent], h0[3][kLateComponent]},
+                acc.dw[0], acc.bh[0]);
 
       // ---- 6. W1^T zbar1, one block at a time, into layer 0 in closed form ----
       // bv is the adjoint of z'_v = c z_v and bj_d that of z'_Jd = 2 W0[:, d], so
