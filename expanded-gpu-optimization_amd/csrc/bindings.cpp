@@ -110,6 +110,8 @@ std::vector<torch::Tensor> forward_saving(torch::Tensor coordinates, torch::Tens
   auto output = torch::empty({batch, 1}, coordinates.options());
   auto laplacian = torch::empty({batch, 1}, coordinates.options());
   const size_t saved_bytes = fhoad_saved_layers_size(batch);
+  TORCH_CHECK(saved_bytes <= static_cast<size_t>(INT64_MAX),
+              "the saved layers of ", batch, " points do not fit in memory");
   auto saved = torch::empty({static_cast<int64_t>(saved_bytes)},
                             coordinates.options().dtype(torch::kUInt8));
   if (batch == 0) {
@@ -248,13 +250,19 @@ struct ModelLaplacian : public torch::autograd::Function<ModelLaplacian> {
     ctx->set_materialize_grads(false);
     ctx->saved_data["backward_version"] = backward_version;
     ctx->saved_data["packed_given"] = packed.has_value();
-    if (save_layers) {
-      std::vector<torch::Tensor> out = forward_saving(coordinates, flat, version);
-      ctx->save_for_backward({coordinates, flat, out[2]});
-      return {out[0], out[1]};
-    }
-    std::vector<torch::Tensor> out = fused_forward_laplacian(coordinates, flat, version);
-    ctx->save_for_backward({coordinates, flat});
+    ctx->saved_data["save_layers"] = save_layers;
+    std::vector<torch::Tensor> out = save_layers ? forward_saving(coordinates, flat, version)
+                                                 : fused_forward_laplacian(coordinates, flat, version);
+    // Saved: coordinates, the packed buffer, the saved layers ("saved" mode) and, when the
+    // buffer is the model's (its parameters are views of it), the ten parameters as well: each
+    // view has its own version counter, so an in-place update of a parameter between this
+    // forward and the backward (an optimizer step before a retain_graph backward) leaves the
+    // buffer's counter alone; saving the views makes autograd's check of their counters raise
+    // PyTorch's in-place-modification error there, as nn.Linear would. Saving copies nothing.
+    std::vector<torch::Tensor> to_save{coordinates, flat};
+    if (save_layers) to_save.push_back(out[2]);
+    if (packed.has_value()) to_save.insert(to_save.end(), parameters.begin(), parameters.end());
+    ctx->save_for_backward(to_save);
     return {out[0], out[1]};
   }
 
@@ -279,7 +287,8 @@ struct ModelLaplacian : public torch::autograd::Function<ModelLaplacian> {
     const auto out = backward_for_autograd(
         saved[0], saved[1], upstream(grads[0]), upstream(grads[1]), needs_coordinates,
         ctx->saved_data["backward_version"].toInt(),
-        saved.size() > 2 ? c10::optional<torch::Tensor>(saved[2]) : c10::nullopt);
+        ctx->saved_data["save_layers"].toBool() ? c10::optional<torch::Tensor>(saved[2])
+                                                : c10::nullopt);
     if (needs_coordinates) result[0] = *out[1];
     if (needs_parameters) {
       const torch::Tensor& grad_flat = *out[0];
@@ -362,7 +371,19 @@ torch::Tensor poisson_adam_step(torch::Tensor coordinates, torch::Tensor source,
   return loss;
 }
 
+// Waits for the device's current stream and raises if a kernel since the last check gave up a
+// bounded wait (fhoad_check_device).
+void check_device(torch::Device device) {
+  TORCH_CHECK(device.is_cuda(), "device must be a CUDA device");
+  const c10::DeviceGuard device_guard(device);
+  check_status(fhoad_check_device(static_cast<void*>(
+      at::hip::getCurrentHIPStreamMasqueradingAsCUDA(device.index()).stream())));
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
+  module.def("_check_device", &check_device,
+             "Raise if a kernel on this device gave up a bounded wait since the last check",
+             pybind11::arg("device"));
   module.def("poisson_adam_step", &poisson_adam_step,
              "Fused Poisson PINN training step with Adam on the packed parameters (MI355X)",
              pybind11::arg("coordinates"), pybind11::arg("source"), pybind11::arg("parameters"),

@@ -610,20 +610,37 @@ __device__ __forceinline__ void load_saved_layer(const f4* __restrict__ saved, i
 // operands in the same order, so both paths give bitwise the same results.
 constexpr int kQuadSpinLimit = 1 << 24;  // about 0.5 s of s_sleep(1); never reached by a whole quad
 
+// Device status word, one per GPU: bit kStatusQuadTimeout is set when a quad meeting gave up
+// (quad_sync below). fhoad_check_device reads and clears it.
+constexpr unsigned kStatusQuadTimeout = 1u;
+__device__ unsigned g_device_status = 0;
+
 // The four waves of a quad each add 1 to `flag` per meeting and wait until it reaches `target`
-// (4 x the meetings so far). The release fence completes the wave's LDS writes before its
-// arrival; the acquire fence orders its later reads after the others' arrivals. Every quad wave
-// takes the same split tiles and meetings, so the wait ends; the spin limit only bounds it.
-__device__ __forceinline__ void quad_sync(unsigned* flag, unsigned target) {
+// (4 x the meetings so far), polling at most `spin_limit` times. The release fence completes the
+// wave's LDS writes before its arrival; the acquire fence orders its later reads after the
+// others' arrivals. Every quad wave takes the same split tiles and meetings, so the wait ends;
+// the limit only bounds it. Returns false when the wave gave up: it then sets
+// kStatusQuadTimeout in the device status word (a global atomic OR) and goes on, and the caller
+// writes NaN for that tile's u and Laplacian.
+__device__ __forceinline__ bool quad_sync(unsigned* flag, unsigned target, int spin_limit) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   if ((threadIdx.x & (kWave - 1)) == 0) {
     __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  for (int spin = 0; spin < kQuadSpinLimit; ++spin) {
-    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+  bool met = false;
+  for (int spin = 0; spin < spin_limit; ++spin) {
+    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) {
+      met = true;
+      break;
+    }
     __builtin_amdgcn_s_sleep(1);
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (!met && (threadIdx.x & (kWave - 1)) == 0) {
+    __hip_atomic_fetch_or(&g_device_status, kStatusQuadTimeout, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return met;
 }
 
 // kSave: also write each tile's hidden-layer outputs to `saved` (saved_index).
@@ -631,7 +648,7 @@ template <int kWaves, bool kSave>
 __global__ void __launch_bounds__(kWaves * kWave)
 forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ params,
                float* __restrict__ output, float* __restrict__ laplacian, int64_t batch,
-               int64_t whole, int64_t tiles, f4* __restrict__ saved) {
+               int64_t whole, int64_t tiles, f4* __restrict__ saved, int spin_limit) {
   __shared__ __attribute__((aligned(16))) float s_wa[3 * kOperandLayerF4 * 4];
   __shared__ __attribute__((aligned(16))) float s_small[kSmallFloats];
   __shared__ f4 s_x[2][4][4][kWave];  // split tiles: [buffer][wave q][component][lane], 32 KB
@@ -680,6 +697,7 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
       }
       f4 h[4][4];
       layer0_forward(s_small, g, x0, x1, h);
+      bool met = true;  // every quad meeting of this tile completed
 #pragma unroll
       for (int layer = 0; layer < 3; ++layer) {
         const f4 bias = lds4(s_small + kSmallBh + layer * kHidden + 16 * q + 4 * g);
@@ -708,7 +726,7 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
 #pragma unroll
         for (int c = 0; c < 4; ++c) buf[q][c][lane] = mine[c];
         meetings += 4;
-        quad_sync(&s_quad, meetings);
+        met = quad_sync(&s_quad, meetings, spin_limit) && met;
         if (layer < 2 || q == 0) {  // after the last layer only wave q = 0 (the output) reads
 #pragma unroll
           for (int ob = 0; ob < 4; ++ob) {
@@ -732,8 +750,10 @@ forward_kernel(const float* __restrict__ coordinates, const float* __restrict__ 
         u = sum_lane_groups(u);
         lap = sum_lane_groups(lap);
         if (g == 0 && active) {
-          output[point] = u + s_small[kSmallBout];
-          laplacian[point] = lap;
+          // A tile whose meetings gave up read stale rows: its outputs are NaN (and the device
+          // status word says why).
+          output[point] = met ? u + s_small[kSmallBout] : __builtin_nanf("");
+          laplacian[point] = met ? lap : __builtin_nanf("");
         }
       }
     }
@@ -2530,9 +2550,22 @@ int noalloc_scratch(void** out) {
   }
   void* address = addresses[device].load(std::memory_order_acquire);
   if (address == nullptr) {
-    err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
-    if (err != hipSuccess || address == nullptr) {
-      return fail(FHOAD_ERROR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(err));
+    // The first call on a device may come while the caller captures a HIP graph (the callers
+    // this entry point is for): the lookup, which may load the code object on this device, runs
+    // in the relaxed capture mode, so a global-mode capture in progress neither rejects it nor
+    // is invalidated by it. The thread's mode is restored afterwards.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    err = hipThreadExchangeStreamCaptureMode(&mode);
+    if (err != hipSuccess) {
+      return fail(FHOAD_ERROR_DEVICE, "hipThreadExchangeStreamCaptureMode: %s", hipGetErrorString(err));
+    }
+    const hipError_t lookup = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    err = hipThreadExchangeStreamCaptureMode(&mode);
+    if (lookup != hipSuccess || address == nullptr) {
+      return fail(FHOAD_ERROR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(lookup));
+    }
+    if (err != hipSuccess) {
+      return fail(FHOAD_ERROR_DEVICE, "hipThreadExchangeStreamCaptureMode: %s", hipGetErrorString(err));
     }
     addresses[device].store(address, std::memory_order_release);
   }
@@ -2568,6 +2601,22 @@ extern "C" const char* fhoad_status_string(int status) {
 
 extern "C" const char* fhoad_last_error(void) { return g_last_error; }
 
+extern "C" int fhoad_check_device(void* stream) {
+  hipError_t err = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(FHOAD_ERROR_DEVICE, "hipStreamSynchronize: %s", hipGetErrorString(err));
+  unsigned status = 0;
+  err = hipMemcpyFromSymbol(&status, HIP_SYMBOL(g_device_status), sizeof(status), 0, hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return fail(FHOAD_ERROR_DEVICE, "reading the device status: %s", hipGetErrorString(err));
+  if (status == 0) return FHOAD_SUCCESS;
+  const unsigned zero = 0;
+  err = hipMemcpyToSymbol(HIP_SYMBOL(g_device_status), &zero, sizeof(zero), 0, hipMemcpyHostToDevice);
+  if (err != hipSuccess) return fail(FHOAD_ERROR_DEVICE, "clearing the device status: %s", hipGetErrorString(err));
+  return fail(FHOAD_ERROR_DEVICE,
+              "a forward split tile's wave gave up waiting for its quad (status 0x%x): that tile's u "
+              "and Laplacian were written as NaN",
+              status);
+}
+
 namespace fhoad {
 namespace {
 
@@ -2600,13 +2649,20 @@ int launch_forward(const float* coordinates, const float* parameters, float* out
     const int forced = std::atoi(env);
     if (forced == 8 || forced == 12) waves = forced;
   }
+  // Polls per quad meeting before a split tile's wave gives up. FUSED_HOAD_QUAD_SPIN_LIMIT
+  // (test knob, read per call) lowers it; 0 makes every meeting give up at once, so the tests can
+  // check the timeout path (device status word, NaN outputs) with every kernel exiting normally.
+  int spin_limit = kQuadSpinLimit;
+  if (const char* env = std::getenv("FUSED_HOAD_QUAD_SPIN_LIMIT")) {
+    spin_limit = static_cast<int>(std::min<long>(std::max<long>(std::atol(env), 0), kQuadSpinLimit));
+  }
   if (waves == 8) {
     hipLaunchKernelGGL((forward_kernel<8, kSave>), dim3(grid), dim3(8 * kWave), 0, hs, coordinates,
-                       parameters, output, laplacian, batch, whole, tiles, saved_f4);
+                       parameters, output, laplacian, batch, whole, tiles, saved_f4, spin_limit);
   } else {
     hipLaunchKernelGGL((forward_kernel<kFwdWaves, kSave>), dim3(grid), dim3(kFwdWaves * kWave), 0,
                        hs, coordinates, parameters, output, laplacian, batch, whole, tiles,
-                       saved_f4);
+                       saved_f4, spin_limit);
   }
   return check_launch("forward_kernel");
 }

@@ -110,12 +110,15 @@ class FlattenedFusedLaplacian(torch.autograd.Function):
     @staticmethod
     def forward(ctx, coordinates: Tensor, flat: Tensor, version: int, *parameters: Tensor):
         ctx.set_materialize_grads(False)
-        ctx.save_for_backward(coordinates, flat)
+        # The parameters are saved too (no copy): each view of the buffer has its own version
+        # counter, so an in-place update between forward and backward raises PyTorch's
+        # in-place-modification error when the backward unpacks them, as nn.Linear would.
+        ctx.save_for_backward(coordinates, flat, *parameters)
         return fused_forward_laplacian(coordinates, flat, version)
 
     @staticmethod
     def backward(ctx, grad_output: Tensor | None, grad_laplacian: Tensor | None):
-        coordinates, flat = ctx.saved_tensors
+        coordinates, flat, *_ = ctx.saved_tensors
         needs_coordinates = ctx.needs_input_grad[0]
         needs_parameters = any(ctx.needs_input_grad[3:])
         if grad_output is None and grad_laplacian is None:

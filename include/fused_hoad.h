@@ -51,6 +51,21 @@ const char* fhoad_status_string(int status);
 const char* fhoad_last_error(void);
 
 /*
+ * Device-side failures that a launch cannot report: waits for `stream` to finish, then reads and
+ * clears the status word of the current device. Returns FHOAD_ERROR_DEVICE with a message when
+ * any kernel since the last check gave up a bounded wait: a forward's split tile (the tiles past
+ * the last whole round, whose rows four waves share) waits for the other three waves at most
+ * about 0.5 s per meeting, and a wave that gives up writes NaN for that tile's u and Laplacian
+ * (and, in fhoad_forward_laplacian_saving, leaves that tile's saved layers undefined). Never
+ * seen in tested runs; FHOAD_SUCCESS otherwise.
+ *
+ * No counterpart in the reference, whose kernels have no bounded waits; its launch errors
+ * surface through C10_CUDA_KERNEL_LAUNCH_CHECK (/root/reference/csrc/fused_residual.cu:641),
+ * as this library's do through each entry point's return code.
+ */
+int fhoad_check_device(void* stream);
+
+/*
  * Forward Laplacian: output[b] = u(x_b) and laplacian[b] = (d2u/dx2 + d2u/dy2)(x_b) for
  * coordinates [batch][2] (x, y interleaved). output and laplacian each hold `batch` floats.
  * version 0..5 is accepted for API compatibility and every value runs the same gfx950

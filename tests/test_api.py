@@ -213,10 +213,14 @@ def test_forward_laplacian_matches_oracle_jet() -> None:
     np.testing.assert_allclose(lap.detach().numpy().ravel(), el, rtol=1e-11, atol=1e-12)
 
 
-def test_forward_laplacian_matches_eager_in_float32() -> None:
-    model, x = _model_and_coordinates(DEFAULT_POISSON_MLP, batch=256, dtype=torch.float32)
-    _, expected = get_backend("eager")(model, x)
-    _, actual = forward_laplacian(model, x)
+@pytest.mark.parametrize("batch", [256, 1024])
+def test_forward_laplacian_matches_eager_in_float32(batch: int) -> None:
+    """1,024 points is BASELINE.json config 1 (the CPU residual), checked at its stated size
+    with the north star's FP32 tolerance."""
+    model, x = _model_and_coordinates(DEFAULT_POISSON_MLP, batch=batch, dtype=torch.float32)
+    eu, expected = get_backend("eager")(model, x)
+    u, actual = forward_laplacian(model, x)
+    torch.testing.assert_close(u, eu, atol=1e-5, rtol=1e-4)
     torch.testing.assert_close(actual, expected, atol=1e-5, rtol=1e-4)
 
 

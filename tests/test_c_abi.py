@@ -60,6 +60,7 @@ def test_header_declares_the_entry_points() -> None:
     assert _declared_functions() == [
         "fhoad_abi_version",
         "fhoad_backward_workspace_size",
+        "fhoad_check_device",
         "fhoad_forward_laplacian",
         "fhoad_forward_laplacian_backward",
         "fhoad_forward_laplacian_backward_noalloc",

@@ -52,7 +52,7 @@ def _pair(batch: int, seed: int = 0, scale: float = 1.0):
 
 
 @pytest.mark.parametrize(
-    "batch", [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 16385, 65536, 65537]
+    "batch", [1, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 1024, 16385, 65536, 65537]
 )
 def test_backward_matches_recompute(batch: int) -> None:
     announce(f"backward vs recompute, batch={batch}")

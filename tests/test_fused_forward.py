@@ -31,11 +31,12 @@ def _fused(x, p, version=2):
 
 
 # the reference's tile edges (test_fused.py:28) plus this kernel's: 16-point wave tiles, and
-# ragged large batches (a partial last tile, workgroups with unequal tile counts)
+# ragged large batches (a partial last tile, workgroups with unequal tile counts); 1,024 and
+# 16,384 are BASELINE.json configs 1 and 2
 @pytest.mark.parametrize(
     "batch",
-    [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 4097, 16384, 16401, 65536, 65537, 70000,
-     100000, 262145],
+    [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 1000, 1024, 4097, 16384, 16401, 65536, 65537,
+     70000, 100000, 262145],
 )
 def test_forward_matches_torch_forward_laplacian(batch: int) -> None:
     announce(f"forward vs torch forward Laplacian, batch={batch}")
@@ -148,6 +149,42 @@ def test_forward_split_rest_is_bitwise_equal_to_whole_tiles(batch: int, scale: f
             u_whole, l_whole = _fused(x, p)
     torch.cuda.synchronize()
     assert torch.equal(u_split, u_whole) and torch.equal(l_split, l_whole)
+
+
+def test_quad_meeting_timeout_is_reported_and_marks_its_tiles() -> None:
+    """A split rest tile's four waves meet at an LDS counter with a bounded wait. With the test
+    knob FUSED_HOAD_QUAD_SPIN_LIMIT=0 every meeting gives up at once (every kernel still runs to
+    its end): the split tiles' u and Laplacian come back NaN, every whole tile's are bitwise the
+    default ones, and _check_device raises once, naming the timeout, then passes again. With the
+    default bound the status word stays clear and the outputs do not change."""
+    from fused_hoad import _C
+
+    batch = 70000  # 4,375 tiles: 279 split tiles past four whole rounds on 256 CUs
+    announce(f"forward quad meeting timeout knob, batch={batch}")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    tiles = (batch + 15) // 16
+    grid = min(tiles, cus)
+    whole = tiles - tiles % (4 * grid) if tiles >= 4 * grid else tiles
+    assert whole < tiles, "the batch must leave split tiles on this device"
+    p = packed(0)
+    x = coordinates(batch, seed=31)
+    device = torch.device("cuda:0")
+    _C._check_device(device)  # clear anything earlier
+    with knobs(FUSED_HOAD_FWD_SPLIT="0"):
+        u_ref, l_ref = _fused(x, p)
+        _C._check_device(device)
+        with knobs(FUSED_HOAD_QUAD_SPIN_LIMIT="0"):
+            u, lap = _fused(x, p)
+        with pytest.raises(RuntimeError, match="gave up waiting for its quad"):
+            _C._check_device(device)
+        _C._check_device(device)  # cleared by the check that reported it
+        split = slice(whole * 16, batch)
+        assert torch.isnan(u[split]).all() and torch.isnan(lap[split]).all()
+        assert torch.equal(u[: whole * 16], u_ref[: whole * 16])
+        assert torch.equal(lap[: whole * 16], l_ref[: whole * 16])
+        u2, l2 = _fused(x, p)
+        _C._check_device(device)
+    assert torch.equal(u2, u_ref) and torch.equal(l2, l_ref)
 
 
 def test_forward_handles_empty_batch() -> None:

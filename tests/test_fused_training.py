@@ -101,6 +101,28 @@ def test_flattened_model_gradients_equal_the_packed_path(loss_kind: str, coordin
         assert torch.equal(got_x, want_x)
 
 
+@pytest.mark.parametrize("mode", ["cuda", "saved", "recompute"])
+def test_in_place_update_before_backward_raises_for_a_flattened_model(mode: str) -> None:
+    """A flattened model's parameters are views of the packed buffer the kernels read. An
+    optimizer step between the forward and a retain_graph backward changes the buffer without
+    changing its version counter; the backward must refuse (PyTorch's in-place-modification
+    error, as nn.Linear gives) instead of differentiating at the new weights. The first
+    backward, before the step, is unaffected."""
+    announce(f"in-place update between forward and backward, flattened model, backward={mode}")
+    from fused_hoad.backends.fused import fused_laplacian
+    from fused_hoad.parameters import flatten_poisson_parameters_
+
+    model = _model(6)
+    flatten_poisson_parameters_(model)
+    optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)
+    _, lap = fused_laplacian(model, coordinates(512, seed=6), backward=mode)
+    loss = lap.pow(2).mean()
+    loss.backward(retain_graph=True)
+    optimizer.step()
+    with pytest.raises(RuntimeError, match="modified by an inplace operation"):
+        loss.backward()
+
+
 @pytest.mark.parametrize("frozen_layers", [(0, 4), (0, 1, 2, 3, 4)])
 @pytest.mark.parametrize("mode", ["cuda", "saved", "recompute"])
 def test_flattened_model_with_frozen_layers(mode: str, frozen_layers: tuple[int, ...]) -> None:

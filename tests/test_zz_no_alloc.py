@@ -93,3 +93,78 @@ def test_noalloc_backward_argument_errors_and_empty_batch() -> None:
     torch.cuda.synchronize()
     assert torch.count_nonzero(gp).item() == 0
     assert np.all(to_numpy64(gp) == 0.0)
+
+
+_CAPTURE_SCRIPT = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, {root!r})
+sys.path.insert(0, {package!r})
+from oracle import torch_ref
+
+lib = ctypes.CDLL({library!r})
+vp, i64, ci = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+lib.fhoad_last_error.restype = ctypes.c_char_p
+lib.fhoad_backward_workspace_size.restype = ctypes.c_size_t
+lib.fhoad_backward_workspace_size.argtypes = [i64]
+lib.fhoad_forward_laplacian_backward.argtypes = [vp, vp, vp, vp, vp, vp, vp, ctypes.c_size_t, i64, ci, vp]
+lib.fhoad_forward_laplacian_backward_noalloc.argtypes = [vp, vp, vp, vp, vp, vp, i64, ci, vp]
+
+batch = 70001
+gen = torch.Generator().manual_seed(77)
+p = torch_ref.pack(torch_ref.reference_model(0)).cuda()
+x = (torch.rand(batch, 2, generator=gen) * 2 - 1).cuda()
+gu = torch.randn(batch, generator=gen).cuda()
+gl = torch.randn(batch, generator=gen).cuda()
+
+def workspace_call(out_p, out_x):
+    ws_bytes = lib.fhoad_backward_workspace_size(batch)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    status = lib.fhoad_forward_laplacian_backward(
+        x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), out_p.data_ptr(),
+        out_x.data_ptr(), ws.data_ptr(), ws_bytes, batch, 6, torch.cuda.current_stream().cuda_stream)
+    assert status == 0, lib.fhoad_last_error()
+
+want_p, want_x = torch.empty(12737, device="cuda"), torch.empty(batch, 2, device="cuda")
+workspace_call(want_p, want_x)
+torch.cuda.synchronize()
+
+got_p, got_x = torch.zeros(12737, device="cuda"), torch.zeros(batch, 2, device="cuda")
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # the process's first no-allocation call, under capture
+    status = lib.fhoad_forward_laplacian_backward_noalloc(
+        x.data_ptr(), p.data_ptr(), gu.data_ptr(), gl.data_ptr(), got_p.data_ptr(),
+        got_x.data_ptr(), batch, 6, torch.cuda.current_stream().cuda_stream)
+assert status == 0, lib.fhoad_last_error()
+for replay in range(3):
+    got_p.fill_(float("nan")); got_x.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(got_p, want_p), f"replay {{replay}}: grad_parameters differ"
+    assert torch.equal(got_x, want_x), f"replay {{replay}}: grad_coordinates differ"
+    other_p, other_x = torch.empty_like(want_p), torch.empty_like(want_x)
+    workspace_call(other_p, other_x)  # eager work between replays
+    torch.cuda.synchronize()
+    assert torch.equal(other_p, want_p)
+print("captured no-allocation backward: 3 replays bitwise equal", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture(tmp_path: Path) -> None:
+    """The callers this entry point is for may make their first call on a device while they
+    capture a HIP graph. In a fresh process (so the scratch address is not yet known) the first
+    no-allocation call happens inside torch.cuda.graph's capture; three replays, with eager
+    workspace-entry-point calls between them, each give bitwise the workspace entry point's
+    gradients at 70,001 points (64-point whole rounds plus split 16-point tiles)."""
+    import subprocess
+    import sys
+
+    require_gpu_extension()
+    announce("noalloc backward: first call inside HIP graph capture (child process), batch=70001")
+    root = Path(__file__).resolve().parents[1]
+    script = tmp_path / "capture_noalloc.py"
+    script.write_text(_CAPTURE_SCRIPT.format(root=str(root), package=str(root / "expanded-gpu-optimization_amd"),
+                                             library=str(LIBRARY)))
+    result = subprocess.run([sys.executable, str(script)], capture_output=True, text=True, timeout=180)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert "3 replays bitwise equal" in result.stdout
