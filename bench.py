@@ -20,6 +20,19 @@ layers, 3 KB per point; the backward reads them instead of re-running the forwar
 ``train_step_no_coordinate_grad_ms`` is the fused step without the coordinate gradient, a
 labelled variant only.
 
+``host_us_per_call`` is host time per call at 64 points (no synchronize inside a loop of 2,000
+calls, the method of the reference's benchmarks/host_overhead.py): the fused call under no_grad
+(the reference quotes 16-20 us, README.md:102) and zero_grad + forward + backward of
+``fused_laplacian`` on a flattened model and on the model as built. ``launches_per_step``
+counts, with torch.profiler as the reference's benchmarks/count_launches.py does, the host launch
+calls and GPU kernels of one drop-in step, one fused step and one graph-replayed fused step at
+the training size.
+
+``cpu_baseline`` times the reference's CPU path on the host's cores: the headline residual in
+the reference's op structure (one stacked [batch, 4, 64] jet with in-place row fix-ups,
+oracle/torch_ref.py forward_laplacian_stacked), the four-matmul restatement beside it, and the
+eager nested-autograd training step.
+
 ``roofline.traffic`` comes from the committed rocprofv3 summary
 profiles/forward_kernel_65536_traffic.json only when that was measured on the kernel source
 this run executes (same SHA-256); otherwise it is null and ``traffic_source`` says why.
@@ -62,7 +75,7 @@ REFERENCE_A5000 = {"residual_points_per_s_64k": 121.9e6, "train_step_ms_64k": 3.
                    "hardware": "RTX A5000", "source": "reference results/2026-11-06-RTX-A5000-8454035"}
 TRAFFIC_FILE = ROOT / "profiles" / "forward_kernel_65536_traffic.json"
 KERNEL_SOURCE = ROOT / "expanded-gpu-optimization_amd" / "csrc" / "fused_hoad_kernels.hip"
-CPU_RESIDUAL_CALLS = 200     # CPU baseline sample sizes (see _cpu_baseline)
+CPU_RESIDUAL_CALLS = 100     # CPU baseline sample sizes (see _cpu_baseline)
 CPU_RESIDUAL_1K_CALLS = 200
 CPU_STEP_CALLS = 40
 
@@ -173,6 +186,86 @@ def _measured_traffic(points: int):
     }
 
 
+def _host_us(fn, calls: int, torch, repeats: int = 5) -> float:
+    """Host time per call in us: `calls` calls with no synchronize inside the loop, divided by
+    `calls` (/root/reference/benchmarks/host_overhead.py:27-35); the median of `repeats` such
+    loops."""
+    samples = []
+    for _ in range(repeats):
+        torch.cuda.synchronize()
+        tick = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        samples.append((time.perf_counter() - tick) * 1e6 / calls)
+        torch.cuda.synchronize()
+    return round(statistics.median(samples), 2)
+
+
+def _host_overheads(torch, device, get_backend, fused_laplacian, flatten) -> dict:
+    """Host time per call at 64 points, where the kernels are short and the host dominates:
+    the reference's fused call (the fused_cuda backend under no_grad, README.md:102 quotes
+    16-20 us on its hosts), and zero_grad + forward + backward of fused_laplacian with a small
+    loss on a flattened model and on the model as built."""
+    from fused_hoad import DEFAULT_POISSON_MLP, build_mlp
+
+    calls = 2000
+    gen = torch.Generator().manual_seed(0)
+    x = (torch.rand(64, 2, generator=gen) * 2 - 1).to(device)
+    torch.manual_seed(0)
+    frozen = build_mlp(DEFAULT_POISSON_MLP).to(device).requires_grad_(False)
+    run = get_backend("fused_cuda")
+    with torch.no_grad():
+        for _ in range(50):
+            run(frozen, x)
+        forward_us = _host_us(lambda: run(frozen, x), calls, torch)
+    result = {"batch": 64, "calls": calls, "forward_no_grad": forward_us}
+    for label, flat in (("forward_backward_flattened", True), ("forward_backward_as_built", False)):
+        torch.manual_seed(0)
+        model = build_mlp(DEFAULT_POISSON_MLP).to(device)
+        if flat:
+            flatten(model)
+
+        def step():
+            model.zero_grad(set_to_none=True)
+            _, lap = fused_laplacian(model, x)
+            lap.pow(2).mean().backward()
+
+        for _ in range(50):
+            step()
+        result[label] = _host_us(step, calls, torch)
+    return result
+
+
+_LAUNCH_MARKERS = ("LaunchKernel", "GraphLaunch", "LaunchCooperativeKernel")
+
+
+def _launch_counts(torch, fn) -> dict:
+    """Host launch calls and GPU kernels of one call of `fn`, counted with torch.profiler as
+    the reference does (/root/reference/benchmarks/count_launches.py:15-38): runtime launch
+    API events on the CPU side, kernel events on the GPU side."""
+    from torch.profiler import ProfilerActivity, profile
+
+    try:
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+            fn()
+            torch.cuda.synchronize()
+        events = prof.events()
+        launch_names = sorted({e.name for e in events if any(k in e.name for k in _LAUNCH_MARKERS)})
+        launches = sum(1 for e in events if any(k in e.name for k in _LAUNCH_MARKERS))
+        device = [e.name for e in events if e.device_type == torch.autograd.DeviceType.CUDA
+                  and "#" not in e.name]  # user annotations (Optimizer.step#...) are not GPU work
+        copies = [n for n in device if n.startswith(("Memcpy", "Memset"))]
+        kernels = [n for n in device if not n.startswith(("Memcpy", "Memset"))]
+        return {"host_launches": launches, "gpu_kernels": len(kernels), "gpu_copies": len(copies),
+                "launch_calls": launch_names,
+                "kernels": sorted({n.split("(")[0][-80:] for n in kernels})}
+    except Exception as err:  # the profiler is a measurement aid: report, do not abort the bench
+        return {"host_launches": None, "gpu_kernels": None, "error": f"{type(err).__name__}: {err}"}
+
+
 def _scaled_error(actual, expected) -> float:
     return float((actual - expected).abs().max() / expected.abs().max().clamp_min(1e-30))
 
@@ -186,7 +279,7 @@ def main() -> None:
 
     import torch
 
-    from fused_hoad import DEFAULT_POISSON_MLP, build_mlp, forward_laplacian, manufactured_source
+    from fused_hoad import DEFAULT_POISSON_MLP, build_mlp, forward_laplacian, get_backend, manufactured_source
     from fused_hoad._extension import (
         fused_forward_laplacian,
         fused_forward_laplacian_backward,
@@ -446,6 +539,30 @@ def main() -> None:
     graph_ms = graph_total_ms / args.steps
     log(f"train step (fused, HIP graph) {args.train_points} pts: {graph_ms:.3f} ms wall/step")
 
+    # ---- host time per call and launches per step (the reference's host_overhead.py and
+    # count_launches.py methods) ----
+    host_us = _host_overheads(torch, device, get_backend, fused_laplacian, flatten_poisson_parameters_)
+    log("host time per call at 64 points (us, median of 5 x 2,000 calls, no sync inside): "
+        + ", ".join(f"{k} {v}" for k, v in host_us.items() if isinstance(v, float)))
+    torch.manual_seed(0)
+    dropin_model = build_mlp(DEFAULT_POISSON_MLP).to(device)
+    flatten_poisson_parameters_(dropin_model)
+    dropin_opt = torch.optim.Adam(dropin_model.parameters(), lr=1e-3)
+
+    def dropin_step():
+        dropin_opt.zero_grad(set_to_none=True)
+        _, lap_t = fused_laplacian(dropin_model, x_train)
+        (lap_t - source).pow(2).mean().backward()
+        dropin_opt.step()
+
+    launches = {
+        "drop_in_step": _launch_counts(torch, dropin_step),
+        "fused_step": _launch_counts(torch, trainer.step),
+        "fused_step_graph": _launch_counts(torch, replay),
+    }
+    log("launches per step (host launch calls / GPU kernels, torch.profiler): "
+        + ", ".join(f"{k} {v.get('host_launches')}/{v.get('gpu_kernels')}" for k, v in launches.items()))
+
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * 2**20 // 4
         src = torch.ones(n, device=device)
@@ -541,15 +658,40 @@ def main() -> None:
         "roofline": roofline,
         "roofline_backward": roofline_backward,
         "roofline_train_step": roofline_train_step,
+        "host_us_per_call": host_us,
+        "launches_per_step": launches,
         "cpu_baseline": cpu_baseline,
         "reference_published": REFERENCE_A5000,
     }
     print(json.dumps(record), flush=True)
 
 
+def _cpu_description() -> dict:
+    """The host CPU as /proc/cpuinfo describes it (model name, vendor, family/model/stepping,
+    MHz), plus the logical CPU count."""
+    fields = {}
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if ":" not in line:
+                if fields:
+                    break  # the first processor's block is enough
+                continue
+            key, value = (part.strip() for part in line.split(":", 1))
+            if key in ("model name", "vendor_id", "cpu family", "model", "stepping", "cpu MHz") and key not in fields:
+                fields[key] = value
+    except OSError:
+        pass
+    model = fields.get("model name", "?")
+    detail = ", ".join(f"{k} {fields[k]}" for k in ("vendor_id", "cpu family", "model", "stepping", "cpu MHz")
+                       if k in fields)
+    return {"cpu_model": f"{model} ({detail})" if detail else model, "os_cpu_count": os.cpu_count()}
+
+
 def _cpu_baseline(torch) -> dict:
     """The reference's CPU path (oracle/torch_ref.py, a restatement of its PyTorch forward
-    Laplacian and eager-autograd training step) on this host's cores, on a bounded sample."""
+    Laplacian and eager-autograd training step) on this host's cores, on a bounded sample. The
+    headline residual is the reference's op structure (forward_laplacian_stacked: one stacked
+    [batch, 4, 64] jet with in-place row fix-ups); the four-matmul restatement is timed beside it."""
     sys.path.insert(0, str(ROOT))
     from oracle import torch_ref
 
@@ -570,37 +712,37 @@ def _cpu_baseline(torch) -> dict:
             samples.append((time.perf_counter() - tick) * 1e3)
         return statistics.median(samples)
 
-    # About 10 s of CPU work in all (the 64K residual about 5 s, the eager step about 5 s on a
-    # 16-thread host), so that the medians are stable and the bench still ends within minutes.
+    # About 15 s of CPU work in all on a 16-thread host (each 64K residual form about 4 s, the
+    # eager step about 5 s), so that the medians are stable and the bench still ends within
+    # minutes.
     with torch.no_grad():
-        res64k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x), 2, CPU_RESIDUAL_CALLS)
-        res1k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x1k), 5, CPU_RESIDUAL_1K_CALLS)
+        stacked64k_ms = median_ms(lambda: torch_ref.forward_laplacian_stacked(flat, x), 2, CPU_RESIDUAL_CALLS)
+        stacked1k_ms = median_ms(lambda: torch_ref.forward_laplacian_stacked(flat, x1k), 5, CPU_RESIDUAL_1K_CALLS)
+        split64k_ms = median_ms(lambda: torch_ref.forward_laplacian(flat, x), 2, CPU_RESIDUAL_CALLS)
     optimizer = torch.optim.Adam(model.parameters(), lr=1e-3)
     source = torch_ref.poisson_source(x)
     step_ms = median_ms(lambda: torch_ref.eager_train_step(model, x, source, optimizer), 2, CPU_STEP_CALLS)
-    cpu_model = "?"
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    log(f"cpu baseline ({threads} threads, os.cpu_count()={os.cpu_count()}, {cpu_model}): "
-        f"forward Laplacian 64K {res64k_ms:.1f} ms, 1K {res1k_ms:.2f} ms; eager step 64K {step_ms:.1f} ms")
+    cpu = _cpu_description()
+    log(f"cpu baseline ({threads} threads, os.cpu_count()={cpu['os_cpu_count']}, {cpu['cpu_model']}): "
+        f"forward Laplacian (stacked jet, the reference's ops) 64K {stacked64k_ms:.1f} ms, 1K {stacked1k_ms:.2f} ms; "
+        f"four-matmul restatement 64K {split64k_ms:.1f} ms; eager step 64K {step_ms:.1f} ms")
     return {
-        "value": round(65536 / (res64k_ms / 1e3), 1),
+        "value": round(65536 / (stacked64k_ms / 1e3), 1),
         "unit": "points/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle/torch_ref.py PyTorch forward Laplacian (u, Lap u) at 65,536 points, median of "
-                  f"{CPU_RESIDUAL_CALLS} calls after 2 warmup ({res64k_ms:.1f} ms/call); 1,024 points: "
-                  f"{res1k_ms:.2f} ms/call (median of {CPU_RESIDUAL_1K_CALLS}); eager nested-autograd + Adam "
+        "sample": f"oracle/torch_ref.py forward_laplacian_stacked (the reference's op structure: one stacked "
+                  f"[batch, 4, 64] jet, in-place row fix-ups) (u, Lap u) at 65,536 points, median of "
+                  f"{CPU_RESIDUAL_CALLS} calls after 2 warmup ({stacked64k_ms:.1f} ms/call); 1,024 points: "
+                  f"{stacked1k_ms:.2f} ms/call (median of {CPU_RESIDUAL_1K_CALLS}); the four-matmul restatement "
+                  f"(forward_laplacian) at 65,536 points: {split64k_ms:.1f} ms/call; eager nested-autograd + Adam "
                   f"train step at 65,536 points: {step_ms:.1f} ms/step (median of {CPU_STEP_CALLS})",
+        "residual_64k_ms": round(stacked64k_ms, 3),
+        "residual_1k_ms": round(stacked1k_ms, 4),
+        "residual_64k_four_matmul_ms": round(split64k_ms, 3),
         "train_step_ms": round(step_ms, 3),
-        "residual_1k_ms": round(res1k_ms, 4),
-        "os_cpu_count": os.cpu_count(),
-        "cpu_model": cpu_model,
+        "os_cpu_count": cpu["os_cpu_count"],
+        "cpu_model": cpu["cpu_model"],
     }
 
 

@@ -19,9 +19,11 @@ through autograd and torch.optim.Adam. `fused_step` is this build's fused traini
 from __future__ import annotations
 
 import argparse
+import contextlib
 import hashlib
 import statistics
 import time
+from collections.abc import Callable, Iterator
 
 import torch
 
@@ -38,61 +40,87 @@ FUSED_STEP = "fused_step"
 _TRAINABLE = ("eager", "forward_laplacian", "fused_cuda", "fused_cuda_bwd_v1", "fused_cuda_recompute")
 
 
+class _TrainingClock:
+    """Wall time spent training: starts at construction (after a device sync) and leaves out
+    what runs inside ``paused()``, which yields the training seconds so far."""
+
+    def __init__(self) -> None:
+        torch.cuda.synchronize()
+        self.seconds = 0.0
+        self._resumed = time.perf_counter()
+
+    @contextlib.contextmanager
+    def paused(self) -> Iterator[float]:
+        torch.cuda.synchronize()
+        self.seconds += time.perf_counter() - self._resumed
+        try:
+            yield self.seconds
+        finally:
+            self._resumed = time.perf_counter()
+
+
+def _stepper(name: str, model: torch.nn.Module, interior: torch.Tensor, boundary: torch.Tensor,
+             lr: float, graph: bool) -> tuple[Callable[[], torch.Tensor], int]:
+    """One training step of backend `name` (optionally replayed from a captured HIP graph) and
+    the number of steps already taken while building it: a captured step's warmup iterations
+    update the model like any other (1 for the fused step, 3 for ``cuda_graph_step``)."""
+    if name == FUSED_STEP:
+        trainer = FusedPoissonAdam(model, interior, boundary=boundary, lr=lr)
+        return (trainer.graphed(warmup=1), 1) if graph else (trainer.step, 0)
+    optimizer = torch.optim.Adam(model.parameters(), lr=lr, capturable=graph)
+    loss_fn = poisson_loss_fn(get_backend(name), model, interior, boundary)
+    if graph:
+        return cuda_graph_step(loss_fn, optimizer), 3
+
+    def eager_step() -> torch.Tensor:
+        optimizer.zero_grad(set_to_none=True)
+        loss = loss_fn()
+        loss.backward()
+        optimizer.step()
+        return loss
+
+    return eager_step, 0
+
+
+def _weights_digest(model: torch.nn.Module) -> str:
+    """First 12 hex digits of the SHA-256 of the parameters' float32 bytes in model order."""
+    flat = torch.cat([p.detach().reshape(-1) for p in model.parameters()]).cpu()
+    return hashlib.sha256(flat.numpy().tobytes()).hexdigest()[:12]
+
+
 def train(name: str, args: argparse.Namespace, seed: int, graph: bool) -> dict:
-    """Train one backend from `seed`. Returns seconds, final loss, final relative L2, a hash
-    of the weights, and the training seconds and step at which relative L2 first dropped below
-    `args.target` (None if never)."""
+    """Train one backend from `seed` for `args.steps` steps, evaluating the relative L2 error
+    every `args.eval_every` steps outside the timed region. Returns the training seconds
+    (building the step and any capture warmup included), the last step's loss, the final
+    relative L2, a hash of the weights, and the training seconds and step count at the first
+    evaluation below `args.target` (None if none was)."""
+    # Seeded draws in the reference's order: model, then interior and boundary points from one
+    # device generator.
     torch.manual_seed(seed)
     model = build_mlp(DEFAULT_POISSON_MLP).cuda()
     generator = torch.Generator(device="cuda").manual_seed(seed)
     interior = torch.rand(args.interior, 2, device="cuda", generator=generator) * 2 - 1
     boundary = boundary_points(args.boundary, device="cuda", generator=generator)
 
-    torch.cuda.synchronize()
-    start = time.perf_counter()
-    done = 0
-    if name == FUSED_STEP:
-        trainer = FusedPoissonAdam(model, interior, boundary=boundary, lr=args.lr)
-        step = trainer.graphed(warmup=1) if graph else trainer.step
-        done = 1 if graph else 0  # the warmup step counts as training
-    else:
-        optimizer = torch.optim.Adam(model.parameters(), lr=args.lr, capturable=graph)
-        loss_fn = poisson_loss_fn(get_backend(name), model, interior, boundary)
-        if graph:
-            step = cuda_graph_step(loss_fn, optimizer)  # its 3 warmup steps count as training
-            done = 3
-        else:
-
-            def step() -> torch.Tensor:
-                optimizer.zero_grad(set_to_none=True)
-                loss = loss_fn()
-                loss.backward()
-                optimizer.step()
-                return loss
-
-    seconds = 0.0
-    hit_seconds: float | None = None
-    hit_step: int | None = None
-    loss = None
-    while done < args.steps:
-        for _ in range(min(args.eval_every, args.steps - done)):
+    clock = _TrainingClock()
+    step, taken = _stepper(name, model, interior, boundary, args.lr, graph)
+    loss: torch.Tensor | None = None
+    first_hit: tuple[float, int] | None = None
+    while taken < args.steps:
+        window = min(args.eval_every, args.steps - taken)
+        for _ in range(window):
             loss = step()
-        done = min(done + args.eval_every, args.steps)
-        torch.cuda.synchronize()
-        seconds += time.perf_counter() - start
-        if hit_seconds is None and relative_l2_error(model) < args.target:
-            hit_seconds, hit_step = seconds, done
-        start = time.perf_counter()
-    digest = hashlib.sha256()
-    for parameter in model.parameters():
-        digest.update(parameter.detach().cpu().numpy().tobytes())
+        taken += window
+        with clock.paused() as elapsed:
+            if first_hit is None and relative_l2_error(model) < args.target:
+                first_hit = (elapsed, taken)
     return {
-        "seconds": seconds,
-        "loss": loss.detach().item() if loss is not None else float("nan"),
+        "seconds": clock.seconds,
+        "loss": float("nan") if loss is None else loss.detach().item(),
         "rel_l2": relative_l2_error(model),
-        "weights": digest.hexdigest()[:12],
-        "hit_seconds": hit_seconds,
-        "hit_step": hit_step,
+        "weights": _weights_digest(model),
+        "hit_seconds": None if first_hit is None else first_hit[0],
+        "hit_step": None if first_hit is None else first_hit[1],
     }
 
 

@@ -9,6 +9,8 @@ never imports it.
   forward_laplacian.py:28-132. The reference stacks (v, J, L) into one [batch, 4, 64] tensor;
   this restatement keeps the four components as separate [batch, 64] tensors, which is the
   same arithmetic (one matmul per component).
+* ``forward_laplacian_stacked``: the same jet in the reference's op structure (one stacked
+  [batch, 4, 64] tensor, in-place row fix-ups), timed as the CPU baseline's headline.
 * ``recompute_backward``: the reference backward (autograd through the PyTorch jet),
   /root/reference/src/fused_hoad/backends/fused.py:76-101.
 * ``eager_laplacian``: nested ``autograd.grad`` Laplacian, /root/reference/src/fused_hoad/
@@ -87,6 +89,33 @@ def forward_laplacian(flat: Tensor, coords: Tensor) -> tuple[Tensor, Tensor]:
     u = jet[0] @ w_out.unsqueeze(1) + b_out
     lap = jet[3] @ w_out.unsqueeze(1)
     return u, lap
+
+
+def forward_laplacian_stacked(flat: Tensor, coords: Tensor) -> tuple[Tensor, Tensor]:
+    """(u, lap), each [batch, 1], in the reference's op structure, for timing its CPU path:
+    one [batch, 4, width] jet (rows v, J0, J1, L), one matmul per layer with the bias added
+    to the value row in place, and the tanh jet as ``s * z`` with the L row and the value row
+    fixed up in place (/root/reference/src/fused_hoad/backends/forward_laplacian.py:52-67,
+    120-132). The arithmetic is that of forward_laplacian grouped differently, so float32
+    results agree to rounding."""
+    w0, b0, hidden, w_out, b_out = _blocks(flat)
+    batch = coords.shape[0]
+    jet = coords.new_zeros(batch, 4, 2)
+    jet[:, 0] = coords
+    jet[:, 1, 0] = 1.0
+    jet[:, 2, 1] = 1.0
+    layers = [(w0, b0), *hidden, (w_out.unsqueeze(0), b_out.reshape(1))]
+    for index, (weight, bias) in enumerate(layers):
+        z = jet @ weight.t()
+        z[:, 0].add_(bias)
+        if index + 1 == len(layers):
+            return z[:, 0], z[:, 3]
+        a = torch.tanh(z[:, :1])
+        s = 1.0 - a * a
+        jet = s * z
+        jet[:, 3:].add_((-2.0 * a * s) * (z[:, 1:3] * z[:, 1:3]).sum(dim=1, keepdim=True))
+        jet[:, :1].copy_(a)
+    raise AssertionError("unreachable")
 
 
 def recompute_backward(flat: Tensor, coords: Tensor, grad_output: Tensor, grad_laplacian: Tensor):

@@ -48,6 +48,38 @@ def test_torch_forward_laplacian_matches_numpy_jet(seed: int, scale: float) -> N
     np.testing.assert_allclose(lt.numpy().ravel(), lap, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("seed,scale", [(0, 1.0), (1, 3.0)])
+def test_stacked_forward_laplacian_matches_numpy_jet(seed: int, scale: float) -> None:
+    """The reference's op structure (stacked jet, in-place row fix-ups), timed as the CPU
+    baseline, against the float64 closed form; and in float32 against the per-component form
+    to rounding."""
+    flat = _flat(seed, scale)
+    x = _coords(40, seed + 9)
+    u, lap = jet.forward(flat, x)
+    us, ls = torch_ref.forward_laplacian_stacked(torch.tensor(flat), torch.tensor(x))
+    np.testing.assert_allclose(us.numpy().ravel(), u, rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(ls.numpy().ravel(), lap, rtol=1e-12, atol=1e-12)
+    f32, x32 = torch.tensor(flat, dtype=torch.float32), torch.tensor(x, dtype=torch.float32)
+    for got, want in zip(torch_ref.forward_laplacian_stacked(f32, x32), torch_ref.forward_laplacian(f32, x32)):
+        torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-4)
+
+
+def test_stacked_forward_laplacian_planted_mistake_is_caught(monkeypatch: pytest.MonkeyPatch) -> None:
+    """A dropped curvature term (the L row's in-place add) in the stacked form is caught."""
+    flat = _flat(0)
+    x = _coords(16, 5)
+    _, lap = jet.forward(flat, x)
+    real_add = torch.Tensor.add_
+
+    def dropped(self, other, *args, **kwargs):
+        return self if self.shape[1:] == (1, 64) else real_add(self, other, *args, **kwargs)
+
+    monkeypatch.setattr(torch.Tensor, "add_", dropped)
+    _, wrong = torch_ref.forward_laplacian_stacked(torch.tensor(flat), torch.tensor(x))
+    monkeypatch.undo()
+    assert not np.allclose(wrong.numpy().ravel(), lap, rtol=1e-6, atol=1e-8)
+
+
 def _eager_gradients(flat: np.ndarray, x: np.ndarray, gu: np.ndarray, gl: np.ndarray):
     p = torch.tensor(flat, requires_grad=True)
     xt = torch.tensor(x, requires_grad=True)
