@@ -1053,6 +1053,11 @@ struct NoEmit {
   __device__ __forceinline__ bool operator()(int, int) const { return false; }
 };
 
+// after() that does nothing.
+struct NoAfter {
+  __device__ __forceinline__ void operator()(int) const {}
+};
+
 // Per-neuron sums over a wave's 16 points without LDS: lane (m, g) holds x for neuron
 // 16 mb + 4 g + r at point m, so summing value k = 4 mb + r over the 16 lanes of row g gives
 // that neuron's total; row_reduce_scatter16 leaves the total of k = m in lane m. Lane (m, g)
@@ -1138,11 +1143,12 @@ __device__ __forceinline__ void tanh_jet_adjoint_h_seed(float v, float hj0, floa
 // so either can fill the other's latencies. The next block's four A operands (16-byte LDS
 // reads) are issued before this block's MFMAs, so no block waits for LDS. w_rows is this
 // lane's row base (68 m + 4 g). emit(mb, k) may issue LDS writes after k-step k (0..15) of
-// block mb's MFMAs (returning whether it did), behind the next block's reads.
-template <typename Emit = NoEmit>
+// block mb's MFMAs (returning whether it did), behind the next block's reads; after(mb) runs once
+// block mb's output is complete (VALU work of the caller that the next block's MFMAs follow).
+template <typename Emit = NoEmit, typename After = NoAfter>
 __device__ __forceinline__ void forward_layer(const float* s_small, const float* w_rows, int layer,
                                               int g, const f4 (&hin)[4][4], f4 (&hout)[4][4],
-                                              Emit emit = Emit{}) {
+                                              Emit emit = Emit{}, After after = After{}) {
   f4 bias[4];
   load_bias(s_small, layer, g, bias);
   const float* w = w_rows + layer * kPlane;
@@ -1174,6 +1180,7 @@ __device__ __forceinline__ void forward_layer(const float* s_small, const float*
     }
     lds_mfma_fence();  // the next block's reads stay ahead of this block's MFMAs
     tanh_jet4(z, hout[mb]);
+    after(mb);
   }
 }
 
@@ -1876,65 +1883,83 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         sb3.wh[e * kPlane + kWRow * (16 * mb + r)] = h2[mb][early_component(e)][r];
         return true;
       };
-      if constexpr (!kSaved) {
-        forward_layer(s_small, s_w + opaque(rows_off), 2, g, h2, h3, stage_h2);
-      } else {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-          for (int step = 0; step < 12; ++step) stage_h2(mb, step);
-        }
-      }
-
-      if (kLoss) {
-        // lap = w_out . L in the forward kernel's order, then the seed.
-        float out = 0.0f;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const f4 wo = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) out = __builtin_fmaf(wo[r], h3[mb][3][r], out);
-        }
-        out = sum_lane_groups(out);
-        const float res = active ? out - f : 0.0f;
-        gl = seed.inv_batch * (2.0f * res);
-        acc.loss += sum_row16(res * res);
-      }
+      auto stage_zbar3 = [&](int mb, int i) {  // write i < 12 of zbar3's early components
+        sb3.wz[(i >> 2) * kPlane + kWRow * (16 * mb + (i & 3))] = h3[mb][early_component(i >> 2)][i & 3];
+      };
 
       // ---- 2. output layer: w_out / b_out gradients, and hidden layer 3's adjoint ----
       // In the scaled jet u = (4 w_out / c) . v' + b_out and lap = (4 w_out / lambda) . L', so
       // dw_out = sum_p (4 gu / c) v' + (4 gl / lambda) L' and the seeds are
       // vbar' = 4 gu w_out / c, Lbar' = 4 gl w_out / lambda, Jbar' = 0. The point sums stay in
       // registers (row_reduce_scatter16). With kLoss, gu = 0 on interior points: the value seed
-      // and the u terms are dropped (their products with zero). h3 becomes zbar3 in place.
-      {
+      // and the u terms are dropped (their products with zero). h3 becomes zbar3 in place, block
+      // by block: in the backward call, whose upstream gradients are inputs, as soon as hidden
+      // layer 3's block is done (its staging writes then drain behind the next block's MFMAs);
+      // in the fused step after the loss, which needs all of h3.
+      float wout_terms[16];
+      auto seed_block = [&](int mb) {
         const float gu_c = gu * (4.0f / kC);
         const float gl_l = gl * (4.0f / kLambda);
-        float wout_terms[16];
+        const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
+        const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const f4 wv = lds4(s_small + kSmallWoutV + 16 * mb + 4 * g);
-          const f4 wl = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
+        for (int r = 0; r < 4; ++r) {
+          wout_terms[4 * mb + r] = kLoss ? gl_l * h3[mb][3][r]
+                                         : __builtin_fmaf(gu_c, h3[mb][0][r], gl_l * h3[mb][3][r]);
+          float bv = kLoss ? 0.0f : gu * wv[r], bj0, bj1, bl = gl * wl[r];
+          tanh_jet_adjoint_h_seed<kLoss>(h3[mb][0][r], h3[mb][1][r], h3[mb][2][r], h3[mb][3][r],
+                                         bv, bj0, bj1, bl);
+          h3[mb][0][r] = bv;
+          h3[mb][1][r] = bj0;
+          h3[mb][2][r] = bj1;
+          h3[mb][3][r] = bl;
+        }
+      };
+      constexpr bool kSeedInLayer3 = !kLoss && !kSaved;
+      if constexpr (kSeedInLayer3) {
+        forward_layer(
+            s_small, s_w + opaque(rows_off), 2, g, h2, h3,
+            [&](int mb, int step) {
+              const bool wrote = stage_h2(mb, step);
+              if (mb > 0 && step < 12) stage_zbar3(mb - 1, step);
+              return wrote || (mb > 0 && step < 12);
+            },
+            seed_block);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            wout_terms[4 * mb + r] = kLoss ? gl_l * h3[mb][3][r]
-                                           : __builtin_fmaf(gu_c, h3[mb][0][r], gl_l * h3[mb][3][r]);
-            float bv = kLoss ? 0.0f : gu * wv[r], bj0, bj1, bl = gl * wl[r];
-            tanh_jet_adjoint_h_seed<kLoss>(h3[mb][0][r], h3[mb][1][r], h3[mb][2][r], h3[mb][3][r],
-                                           bv, bj0, bj1, bl);
-            h3[mb][0][r] = bv;
-            h3[mb][1][r] = bj0;
-            h3[mb][2][r] = bj1;
-            h3[mb][3][r] = bl;
-          }
+        for (int i = 0; i < 12; ++i) stage_zbar3(3, i);
+      } else {
+        if constexpr (!kSaved) {
+          forward_layer(s_small, s_w + opaque(rows_off), 2, g, h2, h3, stage_h2);
+        } else {
 #pragma unroll
-          for (int i = 0; i < 12; ++i) {  // zbar3's early components of this block
-            sb3.wz[(i >> 2) * kPlane + kWRow * (16 * mb + (i & 3))] = h3[mb][early_component(i >> 2)][i & 3];
+          for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+            for (int step = 0; step < 12; ++step) stage_h2(mb, step);
           }
         }
-        acc.wout += row_reduce_scatter16(wout_terms, m_pick);
-        if (!kLoss) acc.bout += sum_row16(gu);
+        if (kLoss) {
+          // lap = w_out . L in the forward kernel's order, then the seed.
+          float out = 0.0f;
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) {
+            const f4 wo = lds4(s_small + kSmallWoutL + 16 * mb + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) out = __builtin_fmaf(wo[r], h3[mb][3][r], out);
+          }
+          out = sum_lane_groups(out);
+          const float res = active ? out - f : 0.0f;
+          gl = seed.inv_batch * (2.0f * res);
+          acc.loss += sum_row16(res * res);
+        }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          seed_block(mb);
+#pragma unroll
+          for (int i = 0; i < 12; ++i) stage_zbar3(mb, i);
+        }
       }
+      acc.wout += row_reduce_scatter16(wout_terms, m_pick);
+      if (!kLoss) acc.bout += sum_row16(gu);
 
       // ---- 3. hidden layer 3: dW3 from (zbar3, h2), then W3^T zbar3 into layer 2's adjoint ----
       // The adjoint's blocks of zbar2 and h1 (dW2's operands) are staged behind the MFMAs of the
