@@ -1006,41 +1006,51 @@ __device__ __forceinline__ void stage_late_write(const StageBases& sb, const f4 
   base[kWRow * (16 * mb + r)] = (i & 1) ? yl[mb][r] : xl[mb][r];
 }
 
-// dW[16 w + ., 16 n + .] += sum over the 64 tile points of zbar_c h_prev_c^T for the components
-// staged in plane pairs (kFirst + i, kFirst + 3 + i), i < kN. Step s of a component reads the A
-// operand zbar[16 w + m][p] and the B operands h_prev[16 n + m][p] for p = 16 s + 4 g + k,
-// k = 0..3 (16-byte reads, one step ahead), and its 16 MFMAs contract over those points; every
-// lane supplies the same points at each step. emit(step, k) issues staging writes after the
-// MFMAs of point k: they follow the next step's reads, so waiting for those reads never waits for
-// them, and they drain behind the MFMAs. With kBias, returns the sum of this lane's reads of the
-// first component (the hidden bias gradient's partial for row 16 w + m when it is zbar_v).
-template <int kFirst, int kN, bool kBias, typename Emit>
-__device__ __forceinline__ float dw_pass(const StageBases& sb, f4 (&dw)[4], Emit emit) {
-  float bias = 0.0f;
-  f4 na, nb[4];
-  auto read = [&](int step, f4& a, f4 (&b)[4]) {
-    const int plane = kFirst + (step >> 2), s = step & 3;
-    a = lds4(sb.ra + plane * kPlane + 16 * s);
+// The five 16-byte operands of one dW step: the A operand zbar[16 w + m][p] and the B operands
+// h_prev[16 n + m][p], n = 0..3, for p = 16 s + 4 g + k, k = 0..3, of the component staged in
+// plane pair (plane, 3 + plane).
+struct DwOperands {
+  f4 a, b[4];
+};
+
+__device__ __forceinline__ DwOperands dw_read(const StageBases& sb, int plane, int s) {
+  DwOperands o;
+  o.a = lds4(sb.ra + plane * kPlane + 16 * s);
 #pragma unroll
-    for (int n = 0; n < 4; ++n) b[n] = lds4(sb.rb + plane * kPlane + 16 * kWRow * n + 16 * s);
-  };
-  read(0, na, nb);
+  for (int n = 0; n < 4; ++n) o.b[n] = lds4(sb.rb + plane * kPlane + 16 * kWRow * n + 16 * s);
+  return o;
+}
+
+// dW[16 w + ., 16 n + .] += sum over the 64 tile points of zbar_c h_prev_c^T for the components
+// staged in plane pairs (kFirst + i, kFirst + 3 + i), i < kN: four steps (point blocks) per
+// component, 16 MFMAs each contracting over the step's points; every lane supplies the same
+// points at each step. `ops` holds the first step's operands on entry and each step reads the
+// next step's; with kNext >= 0 the last step reads the first operands of plane pair kNext into
+// `ops`. emit(step, k) issues staging writes after the MFMAs of point k: they follow the next
+// step's reads, so waiting for those reads never waits for them, and they drain behind the
+// MFMAs. With kBias, returns the sum of this lane's reads of the first component (the hidden bias
+// gradient's partial for row 16 w + m when it is zbar_v).
+template <int kFirst, int kN, bool kBias, int kNext, typename Emit>
+__device__ __forceinline__ float dw_pass(const StageBases& sb, DwOperands& ops, f4 (&dw)[4],
+                                         Emit emit) {
+  float bias = 0.0f;
 #pragma unroll
   for (int step = 0; step < 4 * kN; ++step) {
-    const f4 a = na;
-    f4 b[4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n) b[n] = nb[n];
+    const DwOperands cur = ops;
     if (kBias && step < 4) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) bias += a[k];
+      for (int k = 0; k < 4; ++k) bias += cur.a[k];
     }
-    if (step + 1 < 4 * kN) read(step + 1, na, nb);
+    if (step + 1 < 4 * kN) {
+      ops = dw_read(sb, kFirst + ((step + 1) >> 2), (step + 1) & 3);
+    } else if (kNext >= 0) {
+      ops = dw_read(sb, kNext, 0);
+    }
     lds_mfma_fence();
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
 #pragma unroll
-      for (int n = 0; n < 4; ++n) dw[n] = mfma(a[k], b[n][k], dw[n]);
+      for (int n = 0; n < 4; ++n) dw[n] = mfma(cur.a[k], cur.b[n][k], dw[n]);
       if (emit(step, k)) __builtin_amdgcn_sched_barrier(0);
     }
     lds_mfma_fence();
@@ -1076,14 +1086,18 @@ __device__ __forceinline__ int owned_neuron(int m, int g) { return 16 * (m >> 2)
 __device__ __forceinline__ void staged_dw(const StageBases& sb, const f4 (&xl)[4], const f4 (&yl)[4],
                                           f4 (&dw)[4], float& g_bias) {
   __syncthreads();  // the early components are written
-  g_bias += sum_lane_groups(dw_pass<0, 1, true>(sb, dw, NoEmit{}));
+  DwOperands ops = dw_read(sb, 0, 0);
+  // The first pass's last step reads the second pass's first operands (planes 1 and 4 were
+  // complete at the first barrier), so the second pass does not start by waiting for LDS.
+  g_bias += sum_lane_groups(dw_pass<0, 1, true, 1>(sb, ops, dw, NoEmit{}));
   __syncthreads();  // every wave is done with planes 0 and 3
-  dw_pass<1, 2, false>(sb, dw, [&](int step, int k) {
+  dw_pass<1, 2, false, -1>(sb, ops, dw, [&](int step, int k) {
     stage_late_write(sb, xl, yl, 4 * step + k);
     return true;
   });
   __syncthreads();  // the late component is written
-  dw_pass<0, 1, false>(sb, dw, NoEmit{});
+  ops = dw_read(sb, 0, 0);
+  dw_pass<0, 1, false, -1>(sb, ops, dw, NoEmit{});
 }
 
 // ---- the interior tiles of backward_kernel: the walk back from each layer's tanh-jet output ----
