@@ -1768,6 +1768,66 @@ __device__ __forceinline__ void split_tile(const float* s_w, const float* s_smal
   }
 }
 
+// Phase clock of backward_kernel, compiled only into a measurement build (-DFHOAD_PHASE_CLOCK;
+// the library build reads no clock and every mark below compiles to nothing). Each wave adds
+// the shader-clock cycles (s_memtime) it spends in each phase of its tiles to its row of
+// g_phase_clock and counts its tiles; fhoad_phase_clock_read copies the table out. A clock
+// read waits for the wave's outstanding LDS and scalar loads, so the measured kernel runs
+// somewhat slower than the library's.
+enum ClockField : int {
+  kClockStage,          // kernel start to the end of the parameter staging
+  kClockForward,        // a tile's start: layer 0 and hidden layers 1, 2 (the forward re-run)
+  kClockLayer3,         // hidden layer 3's forward, the loss and output seed, zbar3's staging
+  kClockDw3,            // dW3 (three staged passes)
+  kClockAdjoint3,       // W3^T zbar3 into layer 2's adjoint
+  kClockDw2,            // dW2
+  kClockAdjoint2,       // W2^T zbar2 into layer 1's adjoint, layer 0 rebuilt
+  kClockDw1,            // dW1
+  kClockLayer0,         // W1^T zbar1, layer 0's adjoint, coordinate gradients
+  kClockRest,           // 16-point split tiles past the last whole round
+  kClockBoundary,       // boundary tiles of the fused step
+  kClockPartials,       // the slot's partial row
+  kClockTiles,          // count of 64-point tiles
+  kClockBoundaryTiles,  // count of boundary tiles
+  kClockWallStart,      // s_memrealtime (100 MHz) at the kernel's start
+  kClockWallEnd,        // s_memrealtime after the partial row's stores are issued
+  kClockFields
+};
+constexpr int kClockWorkgroups = 1024;  // rows kept: workgroups 0 .. 1023
+
+#ifdef FHOAD_PHASE_CLOCK
+__device__ unsigned long long g_phase_clock[kClockWorkgroups][kBwdWaves][kClockFields];
+
+struct PhaseClock {
+  unsigned long long last, fields[kClockFields];
+  __device__ __forceinline__ PhaseClock() {
+#pragma unroll
+    for (int i = 0; i < kClockFields; ++i) fields[i] = 0;
+    fields[kClockWallStart] = wall_clock64();
+    last = clock64();
+  }
+  __device__ __forceinline__ void mark(ClockField field) {
+    const unsigned long long now = clock64();
+    fields[field] += now - last;
+    last = now;
+  }
+  __device__ __forceinline__ void count(ClockField field) { fields[field] += 1; }
+  __device__ __forceinline__ void store(int w) {
+    fields[kClockWallEnd] = wall_clock64();
+    if ((threadIdx.x & (kWave - 1)) == 0 && blockIdx.x < kClockWorkgroups) {
+#pragma unroll
+      for (int i = 0; i < kClockFields; ++i) g_phase_clock[blockIdx.x][w][i] = fields[i];
+    }
+  }
+};
+#else
+struct PhaseClock {
+  __device__ __forceinline__ void mark(ClockField) {}
+  __device__ __forceinline__ void count(ClockField) {}
+  __device__ __forceinline__ void store(int) {}
+};
+#endif
+
 // The outputs h1, h2, h3 of the hidden layers stay in registers through the walk back (each
 // layer's zbar replaces its h in place, and hbar is live one 16-row block at a time), so no
 // layer is parked in memory.
@@ -1798,6 +1858,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   const int w = threadIdx.x / kWave;
   const int m = lane & 15;
   const int g = lane >> 4;
+  PhaseClock clock;
   // The first slot's first tile inputs are read before the staging, which hides their latency.
   TileInputs next{0.f, 0.f, 0.f, 0.f};
   if (static_cast<int>(blockIdx.x) < slots) {
@@ -1810,6 +1871,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
   stage_parameters<kBwdWaves * kWave>(params, s_w, s_small, threadIdx.x);
   __syncthreads();
   if (kLoss && blockIdx.x == 0 && threadIdx.x == 0) seed.step[0] = step_count + 1.0f;
+  clock.mark(kClockStage);
 
   // Lane offsets into the LDS arrays. Each use forms its base from an opaque copy: the arrays
   // span more than the 64 KB reach of a DS offset, and hoisted bases would be spilled.
@@ -1889,6 +1951,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         }
         forward_layer(s_small, s_w + opaque(rows_off), 1, g, h1, h2);
       }
+      clock.mark(kClockForward);
       __syncthreads();  // the previous tile's readers of the staging planes are done
       const StageBases sb3 = stage_bases();
       auto stage_h2 = [&](int mb, int step) {
@@ -1974,6 +2037,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       }
       acc.wout += row_reduce_scatter16(wout_terms, m_pick);
       if (!kLoss) acc.bout += sum_row16(gu);
+      clock.mark(kClockLayer3);
 
       // ---- 3. hidden layer 3: dW3 from (zbar3, h2), then W3^T zbar3 into layer 2's adjoint ----
       // The adjoint's blocks of zbar2 and h1 (dW2's operands) are staged behind the MFMAs of the
@@ -1981,6 +2045,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       staged_dw(sb3, {h3[0][kLateComponent], h3[1][kLateComponent], h3[2][kLateComponent], h3[3][kLateComponent]},
                 {h2[0][kLateComponent], h2[1][kLateComponent], h2[2][kLateComponent], h2[3][kLateComponent]},
                 acc.dw[2], acc.bh[2]);
+      clock.mark(kClockDw3);
       __syncthreads();  // every wave is done with the staged planes
       {
         const StageBases sb = stage_bases();
@@ -1990,6 +2055,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       if constexpr (kSaved) {
         if (has_next) load_saved_layer(saved, next_saved_tile, saved_tiles, 2, lane, h3);
       }
+      clock.mark(kClockAdjoint3);
 
       // ---- 4. hidden layer 2: dW2 from (zbar2, h1), then W2^T zbar2 into layer 1's adjoint ----
       // Layer 0's output h0 (dW1's h_prev) is rebuilt block by block from its closed form
@@ -2001,6 +2067,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         staged_dw(sb, {h2[0][kLateComponent], h2[1][kLateComponent], h2[2][kLateComponent], h2[3][kLateComponent]},
                   {h1[0][kLateComponent], h1[1][kLateComponent], h1[2][kLateComponent], h1[3][kLateComponent]},
                   acc.dw[1], acc.bh[1]);
+        clock.mark(kClockDw2);
         deliver(next);  // the next tile's inputs, before this tile's stores
         __syncthreads();  // every wave is done with the staged planes
         adjoint_through(
@@ -2024,12 +2091,14 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       if constexpr (kSaved) {
         if (has_next) load_saved_layer(saved, next_saved_tile, saved_tiles, 1, lane, h2);
       }
+      clock.mark(kClockAdjoint2);
 
       // ---- 5. hidden layer 1: dW1 from (zbar1, h0) ----
       staged_dw(stage_bases(),
                 {h1[0][kLateComponent], h1[1][kLateComponent], h1[2][kLateComponent], h1[3][kLateComponent]},
                 {h0[0][kLateComponent], h0[1][kLateComponent], h0[2][kLateComponent], h0[3][kLateComponent]},
                 acc.dw[0], acc.bh[0]);
+      clock.mark(kClockDw1);
 
       // ---- 6. W1^T zbar1, one block at a time, into layer 0 in closed form ----
       // bv is the adjoint of z'_v = c z_v and bj_d that of z'_Jd = 2 W0[:, d], so
@@ -2077,6 +2146,8 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
           grad_coordinates[2 * point + 1] = gx1;
         }
       }
+      clock.mark(kClockLayer0);
+      clock.count(kClockTiles);
     }
     // kRest: interior points past the last whole round of 64-point tiles, as 16-point tiles
     // whose rows are split over the 4 waves (split_tile), so a round that is not whole costs a
@@ -2121,6 +2192,7 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         }
         deliver(next);
       }
+      clock.mark(kClockRest);
     }
     if (kLoss) {
       for (; tile < tiles; tile += slots) {  // boundary tiles (uniform per workgroup)
@@ -2136,6 +2208,8 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
         boundary_tile(s_w, s_small, s_stage, rows_off, cols_off, w, g, m_pick, in.x0, in.x1,
                       active, seed.boundary_scale, acc);
         deliver(next);
+        clock.mark(kClockBoundary);
+        clock.count(kClockBoundaryTiles);
       }
     }
 
@@ -2180,7 +2254,9 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       }
     }
     __syncthreads();  // s_red and the staging buffer are reused by the next slot
+    clock.mark(kClockPartials);
   }
+  clock.store(w);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -2655,6 +2731,34 @@ extern "C" int fhoad_check_device(void* stream) {
               "and Laplacian were written as NaN",
               status);
 }
+
+#ifdef FHOAD_PHASE_CLOCK
+// Measurement build only: the shape of backward_kernel's phase-clock table
+// ([workgroups][waves][fields] of uint64), its reset and its copy to the host.
+extern "C" void fhoad_phase_clock_shape(int* workgroups, int* waves, int* fields) {
+  *workgroups = kClockWorkgroups;
+  *waves = kBwdWaves;
+  *fields = kClockFields;
+}
+
+extern "C" int fhoad_phase_clock_reset(void) {
+  static const unsigned long long zeros[kClockWorkgroups * kBwdWaves * kClockFields] = {};
+  hipError_t err = hipDeviceSynchronize();
+  if (err == hipSuccess) err = hipMemcpyToSymbol(HIP_SYMBOL(g_phase_clock), zeros, sizeof(zeros));
+  if (err != hipSuccess) return fail(FHOAD_ERROR_DEVICE, "resetting the phase clock: %s", hipGetErrorString(err));
+  return FHOAD_SUCCESS;
+}
+
+extern "C" int fhoad_phase_clock_read(unsigned long long* out) {
+  hipError_t err = hipDeviceSynchronize();
+  if (err == hipSuccess) {
+    err = hipMemcpyFromSymbol(out, HIP_SYMBOL(g_phase_clock), sizeof(g_phase_clock), 0,
+                              hipMemcpyDeviceToHost);
+  }
+  if (err != hipSuccess) return fail(FHOAD_ERROR_DEVICE, "reading the phase clock: %s", hipGetErrorString(err));
+  return FHOAD_SUCCESS;
+}
+#endif
 
 namespace fhoad {
 namespace {

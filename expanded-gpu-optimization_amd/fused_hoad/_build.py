@@ -9,7 +9,8 @@ Two artefacts, both written next to this file so they travel with the source tre
   ``$ORIGIN`` rpath.
 
 Replaces the reference's ``CUDAExtension`` build (/root/reference/setup.py:9-27). Run as
-``python -m fused_hoad._build`` with ``expanded-gpu-optimization_amd`` on ``sys.path``.
+``python -m fused_hoad._build`` with ``expanded-gpu-optimization_amd`` on ``sys.path``;
+``--phase-clock`` builds only the measurement copy of the library that ``phase_clock.py`` runs.
 """
 
 from __future__ import annotations
@@ -27,6 +28,7 @@ CSRC = SOURCE_ROOT / "csrc"
 INCLUDE = SOURCE_ROOT.parent / "include"
 LIBRARY_NAME = "libfused_hoad_hip.so"
 LIBRARY = PACKAGE_DIR / LIBRARY_NAME
+PHASE_CLOCK_LIBRARY = PACKAGE_DIR / "libfused_hoad_hip_phase_clock.so"
 ARCH = "gfx950"
 
 # -packed-fp32-ops keeps hipcc from forming v_pk_*_f32 instructions from scalar float code.
@@ -66,13 +68,20 @@ def _hipcc() -> str:
     return os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compile the HIP kernels and the C ABI into ``libfused_hoad_hip.so``."""
-    tmp = LIBRARY.with_suffix(".so.tmp")
+def build_library(verbose: bool = False, phase_clock: bool = False) -> Path:
+    """Compile the HIP kernels and the C ABI into ``libfused_hoad_hip.so``.
+
+    ``phase_clock`` builds the measurement copy instead, ``libfused_hoad_hip_phase_clock.so``
+    (``-DFHOAD_PHASE_CLOCK``: the backward kernel times its phases; see ``phase_clock.py``).
+    Nothing in the package loads it.
+    """
+    library = PHASE_CLOCK_LIBRARY if phase_clock else LIBRARY
+    tmp = library.with_suffix(".so.tmp")
     _run(
         [
             _hipcc(),
             *HIP_FLAGS,
+            *(["-DFHOAD_PHASE_CLOCK"] if phase_clock else []),
             f"-I{INCLUDE}",
             f"-I{CSRC}",
             str(CSRC / "fused_hoad_kernels.hip"),
@@ -81,8 +90,8 @@ def build_library(verbose: bool = False) -> Path:
         ],
         verbose,
     )
-    tmp.replace(LIBRARY)
-    return LIBRARY
+    tmp.replace(library)
+    return library
 
 
 def build_extension(verbose: bool = False) -> Path:
@@ -136,4 +145,7 @@ def build(verbose: bool = False) -> None:
 
 
 if __name__ == "__main__":
-    build(verbose="-q" not in sys.argv)
+    if "--phase-clock" in sys.argv:
+        build_library(verbose="-q" not in sys.argv, phase_clock=True)
+    else:
+        build(verbose="-q" not in sys.argv)
