@@ -2214,6 +2214,9 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
     }
 
     // ---- this slot's partial row: every entry written by exactly one lane ----
+    // Non-temporal stores: the row is read once, by the reduction kernel, so it is streamed out
+    // at once instead of waiting dirty in L2 for the write-back at the kernel's end (with every
+    // workgroup's row dirty there, that write-back took about 3 us of a short call's tail).
     float* row = partials + static_cast<int64_t>(slot) * kRowStride;
     const int dw_lane = opaque((16 * w + 4 * g) * kHidden + m);
 #pragma unroll
@@ -2222,10 +2225,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wrow[dw_lane + r * kHidden + 16 * nb] = 4.0f * acc.dw[l][nb][r];
+        for (int r = 0; r < 4; ++r) {
+          __builtin_nontemporal_store(4.0f * acc.dw[l][nb][r], &wrow[dw_lane + r * kHidden + 16 * nb]);
+        }
       }
       // dW: the sums are of d/d(4 W); bias sums are of zbar_v' = c^-1 zbar_v.
-      if (g == 0) wrow[kHidden * kHidden + 16 * w + m] = kC * acc.bh[l];
+      if (g == 0) __builtin_nontemporal_store(kC * acc.bh[l], &wrow[kHidden * kHidden + 16 * w + m]);
     }
     // Per-wave sums (lane = owned neuron) combined over the 4 waves in a fixed order.
     __syncthreads();  // every wave is done with the staging buffer
@@ -2246,11 +2251,12 @@ backward_kernel(const float* __restrict__ coordinates, const float* __restrict__
       const float* c4 = comb + q * kBwdWaves * kHidden + n;
       const float total = ((c4[0] + c4[kHidden]) + c4[2 * kHidden]) + c4[3 * kHidden];
       const int dst = q == 0 ? kInputs * n : q == 1 ? kInputs * n + 1 : q == 2 ? kLayer0Bias + n : kOutputBase + n;
-      row[dst] = (q == 2 ? kC : q == 3 ? 1.0f : 2.0f) * total;  // dW0 / 2, db0 / c, dw_out
+      // dW0 / 2, db0 / c, dw_out
+      __builtin_nontemporal_store((q == 2 ? kC : q == 3 ? 1.0f : 2.0f) * total, &row[dst]);
       if (threadIdx.x < (kLoss ? 3 : 1)) {
         const float* red = s_red[threadIdx.x];
         const int col = threadIdx.x == 0 ? kOutputBase + kHidden : kLossColumn + threadIdx.x - 1;
-        row[col] = ((red[0] + red[1]) + red[2]) + red[3];
+        __builtin_nontemporal_store(((red[0] + red[1]) + red[2]) + red[3], &row[col]);
       }
     }
     __syncthreads();  // s_red and the staging buffer are reused by the next slot

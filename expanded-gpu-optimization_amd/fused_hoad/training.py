@@ -52,6 +52,10 @@ def cuda_graph_step(
         graph.replay()
         return static_loss
 
+    # The graph reads and writes the optimizer's state and the tensors loss_fn closes over by
+    # address: the replay function holds them, so they outlive any caller that keeps only it
+    # (freed, their memory would be handed to other tensors under the replays).
+    replay.owners = (loss_fn, optimizer)
     return replay
 
 
@@ -229,6 +233,9 @@ class FusedPoissonAdam:
             graph.replay()
             return static_loss
 
+        # The graph works on this trainer's buffers by address (parameters, Adam moments, step
+        # count, workspace): the replay function holds the trainer so that they outlive it.
+        replay.trainer = self
         return replay
 
     def load_optimizer_state(self, optimizer: torch.optim.Optimizer) -> None:

@@ -32,3 +32,9 @@ def test_driver_trains_every_mode(capsys) -> None:
     # the two eager runs of a seed agree closely (same loss, same Adam, fused kernels)
     eager = {(r[0], r[2]): float(r[4]) for r in rows if r[1] == "no" and r[2] != "med"}
     assert eager[("fused_step", "0")] == pytest.approx(eager[("fused_cuda", "0")], rel=1e-3)
+    # A graph-replayed run takes the same 40 steps (warmup included) as the eager run of its
+    # seed, so it ends at the same loss. The driver keeps only the replay function, so this also
+    # checks that the replay keeps the buffers its graph works on alive.
+    graphed = {(r[0], r[2]): float(r[4]) for r in rows if r[1] == "yes" and r[2] != "med"}
+    for key, loss in graphed.items():
+        assert loss == pytest.approx(eager[key], rel=1e-3), key
