@@ -2391,22 +2391,41 @@ backward_split_kernel(const float* __restrict__ coordinates, const float* __rest
   }
 }
 
-// Column k's total over the slots, complete in the threads of group 0 (columns >= `columns`
-// read nothing and give 0).
-__device__ __forceinline__ float fixed_tree_sum(const float* __restrict__ partials, int slots,
-                                                int k, int columns, float (*s_part)[64],
-                                                int group, int col) {
-  constexpr int kPerGroup = kMaxSlots / kReduceGroups;
+constexpr int kPerGroup = kMaxSlots / kReduceGroups;  // slots per group of the fixed tree
+
+// Column k's entries of group `group`'s slots, in slot order, as loaded: slot and column are
+// clamped to a written row, and fixed_tree_total drops what lies beyond them. The 16 loads are
+// issued unconditionally, where this is called, and waited for once, in fixed_tree_total:
+// behind per-slot branches the compiler had waited for the first load, and for everything
+// issued before it, before it issued the other 15.
+__device__ __forceinline__ void load_group_column(const float* __restrict__ partials, int slots,
+                                                  int k, int columns, int group,
+                                                  float (&v)[kPerGroup]) {
+  const int column = k < columns ? k : 0;
+#pragma unroll
+  for (int i = 0; i < kPerGroup; ++i) {
+    const int slot = group * kPerGroup + i;
+    v[i] = partials[static_cast<int64_t>(slot < slots ? slot : slots - 1) * kRowStride + column];
+  }
+}
+
+// The fixed-tree total of column k from load_group_column's entries: each group's entries in
+// slot order, then the 16 group sums in group order; complete in the threads of group 0. Slots
+// at or beyond `slots` add +0.0f, and a column >= `columns` sums to +0.0f.
+__device__ __forceinline__ float fixed_tree_total(float (&v)[kPerGroup], int slots, int k,
+                                                  int columns, float (*s_part)[64], int group,
+                                                  int col) {
+  // An empty asm that reads and writes the 16 values: the loads cannot sink past it (into
+  // per-slot branches around the selects below), so they stay where they were issued.
+  __asm__ volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),
+                   "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15]));
+  static_assert(kPerGroup == 16, "the asm above names 16 values");
   float acc = 0.0f;
-  if (k < columns) {
-    float v[kPerGroup];
 #pragma unroll
-    for (int i = 0; i < kPerGroup; ++i) {
-      const int slot = group * kPerGroup + i;
-      v[i] = slot < slots ? partials[static_cast<int64_t>(slot) * kRowStride + k] : 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < kPerGroup; ++i) acc += v[i];
+  for (int i = 0; i < kPerGroup; ++i) {
+    const int slot = group * kPerGroup + i;
+    acc += k < columns && slot < slots ? v[i] : 0.0f;
   }
   s_part[group][col] = acc;
   __syncthreads();
@@ -2427,7 +2446,9 @@ reduce_partials_kernel(const float* __restrict__ partials, int slots, float* __r
   const int col = threadIdx.x & 63;
   const int group = threadIdx.x >> 6;
   const int k = blockIdx.x * 64 + col;
-  const float total = fixed_tree_sum(partials, slots, k, kParameterCount, s_part, group, col);
+  float v[kPerGroup];
+  load_group_column(partials, slots, k, kParameterCount, group, v);
+  const float total = fixed_tree_total(v, slots, k, kParameterCount, s_part, group, col);
   if (group == 0 && k < kParameterCount) grad[k] = total;
 }
 
@@ -2468,7 +2489,19 @@ reduce_adam_kernel(const float* __restrict__ partials, int slots, AdamArgs a) {
     v = a.exp_avg_sq[k];
   }
   const float step_count = a.step[0];
-  const float total = fixed_tree_sum(partials, slots, k, kLossColumn + 2, s_part, group, col);
+  float parts[kPerGroup];
+  load_group_column(partials, slots, k, kLossColumn + 2, group, parts);
+  // The bias corrections (two double-precision powers, a long dependent chain) are formed in
+  // the updating wave while the partial rows are in flight, not after their sum.
+  float step_size = 0.0f, bc2_sqrt = 1.0f;
+  if (updates) {
+    const double t = static_cast<double>(step_count);
+    const double bc1 = 1.0 - pow(a.beta1, t);
+    const double bc2 = 1.0 - pow(a.beta2, t);
+    step_size = static_cast<float>(-(a.lr / bc1));
+    bc2_sqrt = static_cast<float>(sqrt(bc2));
+  }
+  const float total = fixed_tree_total(parts, slots, k, kLossColumn + 2, s_part, group, col);
   if (group == 0 && (k == kLossColumn || k == kLossColumn + 1)) s_loss[k - kLossColumn] = total;
   __syncthreads();
   if (group != 0) return;
@@ -2480,11 +2513,6 @@ reduce_adam_kernel(const float* __restrict__ partials, int slots, AdamArgs a) {
   }
   if (!updates) return;
   if (a.grad) a.grad[k] = total;
-  const double t = static_cast<double>(step_count);
-  const double bc1 = 1.0 - pow(a.beta1, t);
-  const double bc2 = 1.0 - pow(a.beta2, t);
-  const float step_size = static_cast<float>(-(a.lr / bc1));
-  const float bc2_sqrt = static_cast<float>(sqrt(bc2));
   const float w1 = static_cast<float>(1.0 - a.beta1);
   const float b2 = static_cast<float>(a.beta2);
   const float w2 = static_cast<float>(1.0 - a.beta2);
