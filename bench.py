@@ -97,6 +97,10 @@ def _parse() -> argparse.Namespace:
     parser.add_argument("--kernels-only", action="store_true",
                         help="after the correctness check, time only the fused forward and backward "
                              "calls (for counter collection); prints no JSON line")
+    parser.add_argument("--no-host-overheads", action="store_true",
+                        help="skip the host-time and launch-count passes (profiled runs: under "
+                             "rocprofv3 --pmc the 2,000-call host-time loop's deep queue of tiny "
+                             "dispatches was aborted with a malformed AQL packet)")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also run a plain device copy of this many MiB (rocprof counter scale)")
     args = parser.parse_args()
@@ -541,27 +545,29 @@ def main() -> None:
 
     # ---- host time per call and launches per step (the reference's host_overhead.py and
     # count_launches.py methods) ----
-    host_us = _host_overheads(torch, device, get_backend, fused_laplacian, flatten_poisson_parameters_)
-    log("host time per call at 64 points (us, median of 5 x 2,000 calls, no sync inside): "
-        + ", ".join(f"{k} {v}" for k, v in host_us.items() if isinstance(v, float)))
-    torch.manual_seed(0)
-    dropin_model = build_mlp(DEFAULT_POISSON_MLP).to(device)
-    flatten_poisson_parameters_(dropin_model)
-    dropin_opt = torch.optim.Adam(dropin_model.parameters(), lr=1e-3)
+    host_us, launches = None, None
+    if not args.no_host_overheads:
+        host_us = _host_overheads(torch, device, get_backend, fused_laplacian, flatten_poisson_parameters_)
+        log("host time per call at 64 points (us, median of 5 x 2,000 calls, no sync inside): "
+            + ", ".join(f"{k} {v}" for k, v in host_us.items() if isinstance(v, float)))
+        torch.manual_seed(0)
+        dropin_model = build_mlp(DEFAULT_POISSON_MLP).to(device)
+        flatten_poisson_parameters_(dropin_model)
+        dropin_opt = torch.optim.Adam(dropin_model.parameters(), lr=1e-3)
 
-    def dropin_step():
-        dropin_opt.zero_grad(set_to_none=True)
-        _, lap_t = fused_laplacian(dropin_model, x_train)
-        (lap_t - source).pow(2).mean().backward()
-        dropin_opt.step()
+        def dropin_step():
+            dropin_opt.zero_grad(set_to_none=True)
+            _, lap_t = fused_laplacian(dropin_model, x_train)
+            (lap_t - source).pow(2).mean().backward()
+            dropin_opt.step()
 
-    launches = {
-        "drop_in_step": _launch_counts(torch, dropin_step),
-        "fused_step": _launch_counts(torch, trainer.step),
-        "fused_step_graph": _launch_counts(torch, replay),
-    }
-    log("launches per step (host launch calls / GPU kernels, torch.profiler): "
-        + ", ".join(f"{k} {v.get('host_launches')}/{v.get('gpu_kernels')}" for k, v in launches.items()))
+        launches = {
+            "drop_in_step": _launch_counts(torch, dropin_step),
+            "fused_step": _launch_counts(torch, trainer.step),
+            "fused_step_graph": _launch_counts(torch, replay),
+        }
+        log("launches per step (host launch calls / GPU kernels, torch.profiler): "
+            + ", ".join(f"{k} {v.get('host_launches')}/{v.get('gpu_kernels')}" for k, v in launches.items()))
 
     if args.calibrate_copy_mib:
         n = args.calibrate_copy_mib * 2**20 // 4

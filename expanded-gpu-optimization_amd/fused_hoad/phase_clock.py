@@ -140,6 +140,10 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--calls", type=int, default=20)
     ap.add_argument("--compare", action="store_true",
                     help="also time the library build's call with HIP events")
+    ap.add_argument("--by-xcd", action="store_true",
+                    help="also print the last call's wave start and end times and shader clock "
+                         "per XCD (workgroup index mod 8: the dispatcher deals workgroups to the "
+                         "8 XCDs round-robin)")
     args = ap.parse_args(argv)
     if args.workload == "backward":
         args.boundary = 0
@@ -161,6 +165,7 @@ def main(argv: list[str] | None = None) -> int:
         run(lib)
         _check(lib, lib.fhoad_phase_clock_read(table), "phase clock read")
         rows = [table[i * fields:(i + 1) * fields] for i in range(workgroups * waves)]
+        last_by_workgroup = [(i // waves, r) for i, r in enumerate(rows) if r[WALL_END] != 0]
         per_call.append([r for r in rows if r[WALL_END] != 0])
     waves_run = len(per_call[0])
 
@@ -205,6 +210,21 @@ def main(argv: list[str] | None = None) -> int:
             if rows:
                 end = statistics.mean((r[WALL_END] - r[WALL_START]) / WALL_MHZ for r in rows)
                 print(f"waves {label}: {len(rows)}, mean wave time {end:.1f} us")
+    if args.by_xcd:
+        t0 = min(r[WALL_START] for _, r in last_by_workgroup)
+        print("\nper XCD, last call (us after the first wave's start; clock = a wave's cycles over "
+              "its wall time):\n")
+        print("| XCD | waves | start | end (min / median / max) | shader clock MHz (median) |")
+        print("|---|---:|---|---|---:|")
+        for xcd in range(8):
+            rows = [r for wg, r in last_by_workgroup if wg % 8 == xcd]
+            if not rows:
+                continue
+            starts = [(r[WALL_START] - t0) / WALL_MHZ for r in rows]
+            ends = sorted((r[WALL_END] - t0) / WALL_MHZ for r in rows)
+            clocks = [sum(r[:len(PHASES)]) / ((r[WALL_END] - r[WALL_START]) / WALL_MHZ) for r in rows]
+            print(f"| {xcd} | {len(rows)} | {min(starts):.1f}-{max(starts):.1f} | {ends[0]:.1f} / "
+                  f"{statistics.median(ends):.1f} / {ends[-1]:.1f} | {statistics.median(clocks):.0f} |")
     return 0
 
 
